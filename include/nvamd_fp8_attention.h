@@ -1,0 +1,145 @@
+/*
+ * C ABI of the MI355X (gfx950) FP8 paged-attention kernels.
+ *
+ * These entry points replace the three Triton launches of nano-vLLM's FP8
+ * attention path; the Python functions that wrap them keep the reference's
+ * names and signatures:
+ *
+ *   nvamd_store_kvcache          <- store_kvcache_kernel[(N,)]            nanovllm/layers/attention.py:40
+ *                                   (wrapper store_kvcache,                nanovllm/layers/attention.py:33-40)
+ *   nvamd_fp8_decode_attention   <- fp8_paged_attention_decode_kernel[grid] nanovllm/kernels/fp8_attention.py:196-206
+ *                                   (wrapper fp8_decode_attention,         nanovllm/kernels/fp8_attention.py:173-207)
+ *   nvamd_fp8_prefill_attention  <- fp8_paged_attention_prefill_kernel[grid] nanovllm/kernels/fp8_attention.py:341-352
+ *                                   (wrapper fp8_prefill_attention,        nanovllm/kernels/fp8_attention.py:314-353)
+ *
+ * Conventions
+ *   - All pointers are device pointers (HIP), except where noted.  No call
+ *     allocates memory or synchronises; every kernel is enqueued on `stream`
+ *     (a hipStream_t, NULL = default stream), so the calls may be captured
+ *     into a HIP graph.
+ *   - bf16 tensors are passed as raw 16-bit storage; FP8 tensors hold OCP
+ *     E4M3FN bytes (torch.float8_e4m3fn).  Integer metadata is int32.
+ *   - head_dim must be 128 for the attention kernels; block_size must be a
+ *     positive multiple of 64.
+ *   - Return value: NVAMD_OK (0) or an NVAMD_ERR_* code; nvamd_last_error()
+ *     then describes the failure (thread-local, valid until the next call
+ *     on the same thread).
+ *   - Workspace: decode and prefill need `*_workspace_bytes()` bytes of
+ *     device memory for split-KV partial results (0 when no split happens).
+ *     Its contents need no initialisation and are scratch after the call.
+ */
+#ifndef NVAMD_FP8_ATTENTION_H_
+#define NVAMD_FP8_ATTENTION_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NVAMD_OK 0
+#define NVAMD_ERR_INVALID_ARGUMENT 1
+#define NVAMD_ERR_UNSUPPORTED 2
+#define NVAMD_ERR_WORKSPACE 3
+#define NVAMD_ERR_LAUNCH 4
+
+/* ABI version of this header (bumped on any signature change). */
+int32_t nvamd_abi_version(void);
+
+/* Description of the last error on the calling thread ("" if none). */
+const char* nvamd_last_error(void);
+
+/*
+ * FP8 KV-cache store / quantise.  Replaces store_kvcache_kernel
+ * (nanovllm/layers/attention.py:11-31, launched at :40).
+ *
+ * key/value: bf16, num_tokens rows of num_kv_heads*head_dim contiguous
+ *   elements (strides (key_stride0, head_dim, 1)), row stride in elements.
+ * k_cache/v_cache: E4M3FN [num_slots, num_kv_heads*head_dim] contiguous
+ *   (num_slots = num_blocks*block_size).
+ * slot_mapping: int32[num_tokens]; -1 skips the row (attention.py:24).
+ *   Slots outside [0, num_slots) are not written.
+ * Rounding: nearest-even to E4M3FN, |x| > 448 saturates to +-448, NaN -> NaN.
+ */
+int32_t nvamd_store_kvcache(const void* key, int64_t key_stride0,
+                            const void* value, int64_t value_stride0,
+                            void* k_cache, void* v_cache,
+                            const int32_t* slot_mapping, int64_t num_tokens,
+                            int32_t num_kv_heads, int32_t head_dim, int64_t num_slots,
+                            void* stream);
+
+/* Workspace needed by nvamd_fp8_decode_attention for these static shapes
+ * (part_tokens = 0 selects the library's partition size). */
+int64_t nvamd_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                                     int32_t max_num_blocks, int32_t block_size,
+                                     int32_t part_tokens);
+
+/*
+ * Paged decode, one query token per sequence.  Replaces
+ * fp8_paged_attention_decode_kernel (nanovllm/kernels/fp8_attention.py:88-171,
+ * launched at :196-206).
+ *
+ * out, q: bf16 [batch, num_heads, head_dim] contiguous (q may have more rows;
+ *   only the first `batch` are used, as in the reference where batch comes
+ *   from block_tables.shape[0]).
+ * k_cache/v_cache: E4M3FN [num_blocks, block_size, num_kv_heads, head_dim].
+ * block_tables: int32 [batch, max_num_blocks] row-major; entries past
+ *   ceil(context_lens[b]/block_size) are never read.
+ * context_lens: int32 [batch].  A row with context 0 is written as zeros
+ *   (the reference produces NaN there).
+ * out = bf16(fp16(softmax(scale * q.K^T) . V)), fp32 accumulation.
+ * part_tokens: split-KV partition length (multiple of 256) or 0 = automatic.
+ */
+int32_t nvamd_fp8_decode_attention(void* out, const void* q,
+                                   const void* k_cache, const void* v_cache,
+                                   const int32_t* block_tables, const int32_t* context_lens,
+                                   int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                                   int32_t head_dim, int64_t num_blocks, int32_t block_size,
+                                   int32_t max_num_blocks, float softmax_scale,
+                                   int32_t part_tokens, void* workspace, int64_t workspace_bytes,
+                                   void* stream);
+
+/* Workspace needed by nvamd_fp8_prefill_attention.  kv_cap is the static
+ * upper bound of keys per sequence: max_num_blocks*block_size for the paged
+ * layout, the number of K/V rows for the contiguous layout. */
+int64_t nvamd_prefill_workspace_bytes(int64_t num_tokens, int32_t num_seqs, int32_t num_heads,
+                                      int32_t num_kv_heads, int64_t kv_cap,
+                                      int32_t max_seqlen_q, int32_t part_tokens);
+
+/*
+ * Varlen causal prefill (chunked prefill over cached context and
+ * speculative-decode verification rows).  Replaces
+ * fp8_paged_attention_prefill_kernel (nanovllm/kernels/fp8_attention.py:209-312,
+ * launched at :341-352).
+ *
+ * q, out: bf16 [num_tokens, num_heads, head_dim] contiguous.
+ * Paged layout (block_tables != NULL): k/v are E4M3FN caches
+ *   [num_kv_rows/block_size, block_size, num_kv_heads, head_dim] and
+ *   block_tables is int32 [num_seqs, max_num_blocks].
+ * Contiguous layout (block_tables == NULL): k/v are E4M3FN
+ *   [num_kv_rows, num_kv_heads, head_dim]; sequence s owns rows
+ *   [cu_seqlens_k[s], cu_seqlens_k[s+1]).
+ * cu_seqlens_q/k: int32 [num_seqs+1].  Query row i of sequence s attends to
+ *   keys j <= i + (Lk - Lq) (bottom-right aligned causal mask).
+ * max_seqlen_q bounds Lq (host value, as in the reference's grid);
+ *   max_seqlen_k is accepted for signature parity and not needed.
+ * Short-query sequences (Lq * num_heads/num_kv_heads <= 32, e.g. speculative
+ * decode verification) run on the split-KV decode kernel; longer ones on
+ * the MFMA prefill kernel.
+ */
+int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, const void* v,
+                                    const int32_t* block_tables,
+                                    const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                    int64_t num_tokens, int32_t num_seqs, int32_t num_heads,
+                                    int32_t num_kv_heads, int32_t head_dim, int64_t num_kv_rows,
+                                    int32_t block_size, int32_t max_num_blocks,
+                                    int32_t max_seqlen_q, int32_t max_seqlen_k,
+                                    float softmax_scale, int32_t part_tokens,
+                                    void* workspace, int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NVAMD_FP8_ATTENTION_H_ */

@@ -1,0 +1,289 @@
+// C ABI entry points (declared in include/nvamd_fp8_attention.h): argument
+// validation, static partition sizing and kernel launches.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "kernels.h"
+#include "nvamd_fp8_attention.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int32_t fail(int32_t code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int32_t fail(int32_t code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int32_t ok() {
+  g_last_error.clear();
+  return NVAMD_OK;
+}
+
+int32_t launch_status(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(NVAMD_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+int device_cu_count() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return 256;
+  return cus;
+}
+
+constexpr int kHeadDim = 128;
+constexpr int kMqMaxCols = 32;        // query rows per kv head packed by the split-KV kernel
+constexpr int kPartAlign = 256;       // partition lengths are multiples of 256 tokens
+constexpr int64_t kPartialFloats = kHeadDim + 2;  // acc[128] + (m, l) per partition
+
+// Split-KV partition length from static shapes only (graph-safe): aim for
+// about 16 workgroups per CU when every sequence is at its capacity.
+int64_t choose_part_tokens(int64_t items, int64_t kv_cap, int64_t requested) {
+  if (requested > 0) return requested;
+  items = std::max<int64_t>(items, 1);
+  const int64_t target = (int64_t)device_cu_count() * 16;
+  const int64_t parts = std::max<int64_t>((target + items - 1) / items, 1);
+  int64_t part = (std::max<int64_t>(kv_cap, 1) + parts - 1) / parts;
+  part = (part + kPartAlign - 1) / kPartAlign * kPartAlign;
+  return std::max<int64_t>(part, kPartAlign);
+}
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+int64_t partial_bytes(int64_t rows, int64_t heads, int64_t max_parts) {
+  if (max_parts <= 1) return 0;
+  return rows * heads * max_parts * kPartialFloats * (int64_t)sizeof(float);
+}
+
+void set_partials(nvamd::MqParams& p, void* workspace) {
+  const int64_t n = p.q_rows * p.Hq * p.max_parts;
+  p.part_acc = static_cast<float*>(workspace);
+  p.part_ml = p.part_acc ? p.part_acc + n * kHeadDim : nullptr;
+}
+
+int32_t check_heads(const char* fn, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim) {
+  if (head_dim != kHeadDim)
+    return fail(NVAMD_ERR_UNSUPPORTED, "%s: head_dim must be %d (got %d)", fn, kHeadDim, head_dim);
+  if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
+    return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: num_heads (%d) must be a positive multiple of num_kv_heads (%d)",
+                fn, num_heads, num_kv_heads);
+  return NVAMD_OK;
+}
+
+// Largest power of two <= 4 dividing g: query heads per prefill workgroup.
+int heads_per_workgroup(int g) {
+  if (g % 4 == 0) return 4;
+  if (g % 2 == 0) return 2;
+  return 1;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t nvamd_abi_version(void) { return 1; }
+
+const char* nvamd_last_error(void) { return g_last_error.c_str(); }
+
+int32_t nvamd_store_kvcache(const void* key, int64_t key_stride0, const void* value,
+                            int64_t value_stride0, void* k_cache, void* v_cache,
+                            const int32_t* slot_mapping, int64_t num_tokens, int32_t num_kv_heads,
+                            int32_t head_dim, int64_t num_slots, void* stream) {
+  if (num_tokens < 0 || num_kv_heads <= 0 || head_dim <= 0 || num_slots < 0)
+    return fail(NVAMD_ERR_INVALID_ARGUMENT, "store_kvcache: bad sizes (N=%lld Hkv=%d D=%d slots=%lld)",
+                (long long)num_tokens, num_kv_heads, head_dim, (long long)num_slots);
+  if (num_tokens == 0) return ok();
+  if (!key || !value || !k_cache || !v_cache || !slot_mapping)
+    return fail(NVAMD_ERR_INVALID_ARGUMENT, "store_kvcache: null pointer");
+  const int row = num_kv_heads * head_dim;
+  const bool vec = (row % 16 == 0) && (key_stride0 % 8 == 0) && (value_stride0 % 8 == 0) &&
+                   ((uintptr_t)key % 16 == 0) && ((uintptr_t)value % 16 == 0) &&
+                   ((uintptr_t)k_cache % 16 == 0) && ((uintptr_t)v_cache % 16 == 0);
+  return launch_status(nvamd::launch_kv_store(key, key_stride0, value, value_stride0, k_cache, v_cache,
+                                              slot_mapping, num_tokens, row, num_slots, vec,
+                                              (hipStream_t)stream),
+                       "store_kvcache");
+}
+
+int64_t nvamd_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                                     int32_t max_num_blocks, int32_t block_size, int32_t part_tokens) {
+  if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || max_num_blocks <= 0 || block_size <= 0)
+    return 0;
+  const int64_t kv_cap = (int64_t)max_num_blocks * block_size;
+  const int64_t part = choose_part_tokens((int64_t)batch * num_kv_heads, kv_cap, part_tokens);
+  return partial_bytes(batch, num_heads, ceil_div(kv_cap, part));
+}
+
+int32_t nvamd_fp8_decode_attention(void* out, const void* q, const void* k_cache, const void* v_cache,
+                                   const int32_t* block_tables, const int32_t* context_lens,
+                                   int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                                   int32_t head_dim, int64_t num_blocks, int32_t block_size,
+                                   int32_t max_num_blocks, float softmax_scale, int32_t part_tokens,
+                                   void* workspace, int64_t workspace_bytes, void* stream) {
+  static const char* fn = "fp8_decode_attention";
+  if (int32_t e = check_heads(fn, num_heads, num_kv_heads, head_dim)) return e;
+  if (batch < 0 || num_blocks < 0 || max_num_blocks < 0)
+    return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: negative size", fn);
+  if (block_size <= 0 || block_size % 64 != 0)
+    return fail(NVAMD_ERR_UNSUPPORTED, "%s: block_size must be a positive multiple of 64 (got %d)", fn, block_size);
+  if (part_tokens < 0 || part_tokens % kPartAlign != 0)
+    return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: part_tokens must be 0 or a multiple of %d", fn, kPartAlign);
+  const int G = num_heads / num_kv_heads;
+  if (G > kMqMaxCols)
+    return fail(NVAMD_ERR_UNSUPPORTED, "%s: more than %d query heads per kv head", fn, kMqMaxCols);
+  if (batch == 0) return ok();
+  if (max_num_blocks == 0)
+    return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: block_tables has no columns", fn);
+  if (!out || !q || !k_cache || !v_cache || !block_tables || !context_lens)
+    return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+
+  nvamd::MqParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint8_t*>(k_cache);
+  p.v = static_cast<const uint8_t*>(v_cache);
+  p.block_tables = block_tables;
+  p.bt_stride = max_num_blocks;
+  p.context_lens = context_lens;
+  p.cu_q = p.cu_k = nullptr;
+  p.out = static_cast<uint16_t*>(out);
+  p.q_rows = batch;
+  p.kv_rows = num_blocks * block_size;
+  p.num_seqs = batch;
+  p.Hq = num_heads;
+  p.Hkv = num_kv_heads;
+  p.G = G;
+  p.block_size = block_size;
+  const int64_t kv_cap = (int64_t)max_num_blocks * block_size;
+  const int64_t part = choose_part_tokens((int64_t)batch * num_kv_heads, kv_cap, part_tokens);
+  p.part_tokens = (int)part;
+  p.max_parts = (int)ceil_div(kv_cap, part);
+  p.mq_max_q = 1;
+  p.scale_log2 = softmax_scale * 1.4426950408889634f;
+  const int64_t need = partial_bytes(p.q_rows, p.Hq, p.max_parts);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail(NVAMD_ERR_WORKSPACE, "%s: workspace of %lld bytes required (got %lld)", fn,
+                (long long)need, (long long)workspace_bytes);
+  set_partials(p, need > 0 ? workspace : nullptr);
+  const int ncb = (G + 15) / 16;
+  return launch_status(nvamd::launch_paged_mq(p, ncb, (hipStream_t)stream), fn);
+}
+
+int64_t nvamd_prefill_workspace_bytes(int64_t num_tokens, int32_t num_seqs, int32_t num_heads,
+                                      int32_t num_kv_heads, int64_t kv_cap, int32_t max_seqlen_q,
+                                      int32_t part_tokens) {
+  if (num_tokens <= 0 || num_seqs <= 0 || num_heads <= 0 || num_kv_heads <= 0 || kv_cap <= 0) return 0;
+  const int G = num_heads / num_kv_heads;
+  if (G <= 0 || G > kMqMaxCols) return 0;
+  (void)max_seqlen_q;
+  const int64_t part = choose_part_tokens((int64_t)num_seqs * num_kv_heads, kv_cap, part_tokens);
+  return partial_bytes(num_tokens, num_heads, ceil_div(kv_cap, part));
+}
+
+int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, const void* v,
+                                    const int32_t* block_tables, const int32_t* cu_seqlens_q,
+                                    const int32_t* cu_seqlens_k, int64_t num_tokens, int32_t num_seqs,
+                                    int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                    int64_t num_kv_rows, int32_t block_size, int32_t max_num_blocks,
+                                    int32_t max_seqlen_q, int32_t max_seqlen_k, float softmax_scale,
+                                    int32_t part_tokens, void* workspace, int64_t workspace_bytes,
+                                    void* stream) {
+  static const char* fn = "fp8_prefill_attention";
+  (void)max_seqlen_k;
+  if (int32_t e = check_heads(fn, num_heads, num_kv_heads, head_dim)) return e;
+  if (num_tokens < 0 || num_seqs < 0 || num_kv_rows < 0 || max_seqlen_q < 0)
+    return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: negative size", fn);
+  const bool paged = block_tables != nullptr;
+  if (paged && (block_size <= 0 || block_size % 64 != 0))
+    return fail(NVAMD_ERR_UNSUPPORTED, "%s: block_size must be a positive multiple of 64 (got %d)", fn, block_size);
+  if (paged && max_num_blocks <= 0)
+    return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: block_tables has no columns", fn);
+  if (part_tokens < 0 || part_tokens % kPartAlign != 0)
+    return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: part_tokens must be 0 or a multiple of %d", fn, kPartAlign);
+  const int G = num_heads / num_kv_heads;
+  if (G > kMqMaxCols)
+    return fail(NVAMD_ERR_UNSUPPORTED, "%s: more than %d query heads per kv head", fn, kMqMaxCols);
+  if (num_tokens == 0 || num_seqs == 0 || max_seqlen_q == 0) return ok();
+  if (!out || !q || !k || !v || !cu_seqlens_q || !cu_seqlens_k)
+    return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+
+  const int mq_max_q = kMqMaxCols / G;
+  const int64_t kv_cap = paged ? (int64_t)max_num_blocks * block_size : std::max<int64_t>(num_kv_rows, 1);
+
+  // Short-query sequences: split-KV multi-query kernel.
+  {
+    nvamd::MqParams p{};
+    p.q = static_cast<const uint16_t*>(q);
+    p.k = static_cast<const uint8_t*>(k);
+    p.v = static_cast<const uint8_t*>(v);
+    p.block_tables = block_tables;
+    p.bt_stride = paged ? max_num_blocks : 0;
+    p.context_lens = nullptr;
+    p.cu_q = cu_seqlens_q;
+    p.cu_k = cu_seqlens_k;
+    p.out = static_cast<uint16_t*>(out);
+    p.q_rows = num_tokens;
+    p.kv_rows = num_kv_rows;
+    p.num_seqs = num_seqs;
+    p.Hq = num_heads;
+    p.Hkv = num_kv_heads;
+    p.G = G;
+    p.block_size = paged ? block_size : 64;
+    const int64_t part = choose_part_tokens((int64_t)num_seqs * num_kv_heads, kv_cap, part_tokens);
+    p.part_tokens = (int)part;
+    p.max_parts = (int)ceil_div(kv_cap, part);
+    p.mq_max_q = std::min(mq_max_q, max_seqlen_q);
+    p.scale_log2 = softmax_scale * 1.4426950408889634f;
+    const int64_t need = partial_bytes(p.q_rows, p.Hq, p.max_parts);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+      return fail(NVAMD_ERR_WORKSPACE, "%s: workspace of %lld bytes required (got %lld)", fn,
+                  (long long)need, (long long)workspace_bytes);
+    set_partials(p, need > 0 ? workspace : nullptr);
+    const int ncb = (G * p.mq_max_q + 15) / 16;
+    hipError_t e = nvamd::launch_paged_mq(p, ncb, (hipStream_t)stream);
+    if (e != hipSuccess) return launch_status(e, fn);
+  }
+
+  // Longer sequences: MFMA prefill kernel.
+  if (max_seqlen_q > mq_max_q) {
+    nvamd::PrefillParams p{};
+    p.q = static_cast<const uint16_t*>(q);
+    p.k = static_cast<const uint8_t*>(k);
+    p.v = static_cast<const uint8_t*>(v);
+    p.block_tables = block_tables;
+    p.bt_stride = paged ? max_num_blocks : 0;
+    p.cu_q = cu_seqlens_q;
+    p.cu_k = cu_seqlens_k;
+    p.out = static_cast<uint16_t*>(out);
+    p.q_rows = num_tokens;
+    p.kv_rows = num_kv_rows;
+    p.num_seqs = num_seqs;
+    p.Hq = num_heads;
+    p.Hkv = num_kv_heads;
+    p.G = G;
+    p.GW = heads_per_workgroup(G);
+    p.BM = 128 / p.GW;
+    p.n_hgroups = G / p.GW;
+    p.n_mblocks = (int)ceil_div(max_seqlen_q, p.BM);
+    p.block_size = paged ? block_size : 64;
+    p.mq_max_q = mq_max_q;
+    p.scale_log2 = softmax_scale * 1.4426950408889634f;
+    hipError_t e = nvamd::launch_varlen_prefill(p, (hipStream_t)stream);
+    if (e != hipSuccess) return launch_status(e, fn);
+  }
+  return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,110 @@
+// Shared device helpers for the gfx950 FP8 paged-attention kernels.
+//
+// Numerical contract (nanovllm/layers/attention.py:27-31 and
+// nanovllm/kernels/fp8_attention.py:147-150,169,311):
+//   * KV values are stored as OCP FP8 E4M3FN with scale 1, rounded to nearest
+//     even; magnitudes beyond 448 saturate to +-448, NaN stays NaN.
+//   * FP8 -> bf16 is exact (every E4M3FN value is a bf16 value), so the MFMA
+//     operands carry the cache values unchanged.
+//   * Outputs are written as bf16(fp16(x)), the reference's double rounding.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nvamd {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kHeadDim = 128;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// ---------------------------------------------------------------------------
+// FP8 <-> wider types
+// ---------------------------------------------------------------------------
+
+// Two E4M3FN bytes held in the low (HI=false) or high (HI=true) 16 bits of w
+// -> two bf16 packed in one dword (element 0 = lower byte).  Exact.
+template <bool HI>
+__device__ __forceinline__ uint32_t fp8x2_to_bf16x2(uint32_t w) {
+  bf16x2 r = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI);
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+// Four E4M3FN bytes -> bf16 x4 as two dwords.
+__device__ __forceinline__ u32x2 fp8x4_to_bf16x4(uint32_t w) {
+  u32x2 r;
+  r.x = fp8x2_to_bf16x2<false>(w);
+  r.y = fp8x2_to_bf16x2<true>(w);
+  return r;
+}
+
+// Saturating clamp applied before the hardware RNE conversion: |x| > 448
+// (including inf) -> +-448; NaN passes through unchanged.
+__device__ __forceinline__ float e4m3_satfinite(float x) {
+  const float ax = __builtin_fabsf(x);
+  return (ax > 448.0f) ? __builtin_copysignf(448.0f, x) : x;
+}
+
+// Four floats -> four E4M3FN bytes (RNE, satfinite) in one dword.
+__device__ __forceinline__ uint32_t f32x4_to_fp8x4(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(e4m3_satfinite(a), e4m3_satfinite(b), 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(e4m3_satfinite(c), e4m3_satfinite(d), w, true);
+  return (uint32_t)w;
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
+  return __builtin_bit_cast(float, bits16 << 16);
+}
+
+// fp32 -> bf16 bits, round to nearest even (finite inputs).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+}
+
+// The reference stores fp16(acc / l) into a bf16 tensor: fp32 -> fp16 (RNE)
+// -> bf16 (RNE).  Returns the bf16 bits.
+__device__ __forceinline__ uint32_t out_round_bf16_bits(float x) {
+  const _Float16 h = (_Float16)x;
+  const float hf = (float)h;
+  uint32_t u = __builtin_bit_cast(uint32_t, hf);
+  if ((u & 0x7F800000u) == 0x7F800000u) return u >> 16;  // inf / NaN keep their class
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// ---------------------------------------------------------------------------
+// Wave-level helpers (wave64)
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float shfl_xor_f32(float v, int mask) {
+  return __shfl_xor(v, mask, 64);
+}
+
+__device__ __forceinline__ int wave_uniform(int v) {
+  return __builtin_amdgcn_readfirstlane(v);
+}
+
+// bf16x8 from four packed dwords.
+__device__ __forceinline__ bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  u32x4 t = {a, b, c, d};
+  return __builtin_bit_cast(bf16x8, t);
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 t) {
+  return __builtin_bit_cast(bf16x8, t);
+}
+
+}  // namespace nvamd

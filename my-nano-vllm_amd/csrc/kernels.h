@@ -1,0 +1,64 @@
+// Kernel parameter blocks and launchers shared by the C-ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nvamd {
+
+// Paged decode / short-query attention (split-KV).
+struct MqParams {
+  const uint16_t* q;            // bf16 [q_rows, Hq, 128]
+  const uint8_t* k;             // FP8: paged [P, bs, Hkv, 128] or contiguous [Nk, Hkv, 128]
+  const uint8_t* v;
+  const int32_t* block_tables;  // [num_seqs, bt_stride]; nullptr = contiguous layout
+  int64_t bt_stride;
+  const int32_t* context_lens;  // decode mode: [num_seqs]
+  const int32_t* cu_q;          // varlen mode: [num_seqs + 1] (nullptr in decode mode)
+  const int32_t* cu_k;
+  uint16_t* out;                // bf16 [q_rows, Hq, 128]
+  float* part_acc;              // [q_rows * Hq, max_parts, 128]
+  float* part_ml;               // [q_rows * Hq, max_parts, 2]
+  int64_t q_rows;               // rows of q / out
+  int64_t kv_rows;              // K/V token rows addressable (P*bs or Nk)
+  int num_seqs;
+  int Hq, Hkv, G;
+  int block_size;
+  int part_tokens, max_parts;
+  int mq_max_q;                 // varlen mode: only sequences with 1 <= Lq <= mq_max_q
+  float scale_log2;
+};
+
+// Varlen causal prefill (long query blocks).
+struct PrefillParams {
+  const uint16_t* q;
+  const uint8_t* k;
+  const uint8_t* v;
+  const int32_t* block_tables;
+  int64_t bt_stride;
+  const int32_t* cu_q;
+  const int32_t* cu_k;
+  uint16_t* out;
+  int64_t q_rows;
+  int64_t kv_rows;
+  int num_seqs;
+  int Hq, Hkv, G;
+  int GW;         // query heads per workgroup
+  int BM;         // query tokens per workgroup (128 / GW)
+  int n_hgroups;  // G / GW
+  int n_mblocks;  // ceil(max_seqlen_q / BM)
+  int block_size;
+  int mq_max_q;   // sequences with Lq <= mq_max_q are left to the short-query kernel
+  float scale_log2;
+};
+
+hipError_t launch_kv_store(const void* key, int64_t key_stride, const void* value,
+                           int64_t value_stride, void* k_cache, void* v_cache,
+                           const int32_t* slot_mapping, int64_t num_tokens, int row_elems,
+                           int64_t num_slots, bool vec, hipStream_t stream);
+
+hipError_t launch_paged_mq(const MqParams& p, int ncb, hipStream_t stream);
+
+hipError_t launch_varlen_prefill(const PrefillParams& p, hipStream_t stream);
+
+}  // namespace nvamd

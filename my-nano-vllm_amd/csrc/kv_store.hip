@@ -1,0 +1,87 @@
+// FP8 E4M3FN KV-cache store / quantise for gfx950.
+//
+// Replaces store_kvcache_kernel (nanovllm/layers/attention.py:11-31): for
+// every token i with slot_mapping[i] != -1, the D = Hkv*head_dim bf16 values of
+// key[i] and value[i] are rounded to E4M3FN and written to
+// cache[slot*D : slot*D + D].
+//
+// Design: purely HBM-bound (2 B read + 1 B written per element).  One lane
+// owns 16 consecutive elements of one row: two 16-byte loads, eight
+// v_cvt_pk_fp8_f32 and one 16-byte store, so a wave moves 1 KiB of bf16 per
+// load instruction.  Lanes of a wave cover consecutive 16-element chunks of
+// the same row (K row first, then the V row), so every load/store
+// instruction is fully coalesced.  Cache offsets are 64-bit (the reference's
+// int32 slot*D wraps once slot*D >= 2**31).
+#include "fp8_common.h"
+#include "kernels.h"
+
+namespace nvamd {
+
+// VEC: rows are 16-byte aligned and D % 16 == 0 (the normal case: K/V are
+// views of the fused qkv projection); otherwise one element per lane-step.
+template <bool VEC>
+__global__ __launch_bounds__(256) void kv_store_fp8_kernel(
+    const uint16_t* __restrict__ key, int64_t key_stride,
+    const uint16_t* __restrict__ value, int64_t value_stride,
+    uint8_t* __restrict__ k_cache, uint8_t* __restrict__ v_cache,
+    const int32_t* __restrict__ slot_mapping, int64_t num_tokens, int row_elems,
+    int64_t num_slots) {
+  const int per_lane = VEC ? 16 : 1;
+  const int64_t chunks_per_row = row_elems / per_lane;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = num_tokens * 2 * chunks_per_row;
+  if (idx >= total) return;
+  const int64_t tok = idx / (2 * chunks_per_row);
+  const int64_t rem = idx - tok * 2 * chunks_per_row;
+  const bool is_v = rem >= chunks_per_row;
+  const int64_t ch = is_v ? rem - chunks_per_row : rem;
+
+  const int32_t slot = slot_mapping[tok];
+  if (slot < 0 || (int64_t)slot >= num_slots) return;  // -1: padding row (attention.py:24)
+
+  const uint16_t* src = (is_v ? value + tok * value_stride : key + tok * key_stride) + ch * per_lane;
+  uint8_t* dst = (is_v ? v_cache : k_cache) + (int64_t)slot * row_elems + ch * per_lane;
+
+  if constexpr (VEC) {
+    const u32x4 a = *reinterpret_cast<const u32x4*>(src);
+    const u32x4 b = *reinterpret_cast<const u32x4*>(src + 8);
+    u32x4 o;
+    o.x = f32x4_to_fp8x4(bf16_bits_to_f32(a.x & 0xFFFFu), bf16_bits_to_f32(a.x >> 16),
+                         bf16_bits_to_f32(a.y & 0xFFFFu), bf16_bits_to_f32(a.y >> 16));
+    o.y = f32x4_to_fp8x4(bf16_bits_to_f32(a.z & 0xFFFFu), bf16_bits_to_f32(a.z >> 16),
+                         bf16_bits_to_f32(a.w & 0xFFFFu), bf16_bits_to_f32(a.w >> 16));
+    o.z = f32x4_to_fp8x4(bf16_bits_to_f32(b.x & 0xFFFFu), bf16_bits_to_f32(b.x >> 16),
+                         bf16_bits_to_f32(b.y & 0xFFFFu), bf16_bits_to_f32(b.y >> 16));
+    o.w = f32x4_to_fp8x4(bf16_bits_to_f32(b.z & 0xFFFFu), bf16_bits_to_f32(b.z >> 16),
+                         bf16_bits_to_f32(b.w & 0xFFFFu), bf16_bits_to_f32(b.w >> 16));
+    *reinterpret_cast<u32x4*>(dst) = o;
+  } else {
+    const float f = bf16_bits_to_f32(*src);
+    const int w = __builtin_amdgcn_cvt_pk_fp8_f32(e4m3_satfinite(f), 0.0f, 0, false);
+    *dst = (uint8_t)(w & 0xFF);
+  }
+}
+
+hipError_t launch_kv_store(const void* key, int64_t key_stride, const void* value,
+                           int64_t value_stride, void* k_cache, void* v_cache,
+                           const int32_t* slot_mapping, int64_t num_tokens, int row_elems,
+                           int64_t num_slots, bool vec, hipStream_t stream) {
+  if (num_tokens == 0) return hipSuccess;
+  const int per_lane = vec ? 16 : 1;
+  const int64_t total = num_tokens * 2 * (row_elems / per_lane);
+  const int64_t blocks = (total + 255) / 256;
+  if (vec) {
+    hipLaunchKernelGGL(kv_store_fp8_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       (const uint16_t*)key, key_stride, (const uint16_t*)value, value_stride,
+                       (uint8_t*)k_cache, (uint8_t*)v_cache, slot_mapping, num_tokens, row_elems,
+                       num_slots);
+  } else {
+    hipLaunchKernelGGL(kv_store_fp8_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       (const uint16_t*)key, key_stride, (const uint16_t*)value, value_stride,
+                       (uint8_t*)k_cache, (uint8_t*)v_cache, slot_mapping, num_tokens, row_elems,
+                       num_slots);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace nvamd

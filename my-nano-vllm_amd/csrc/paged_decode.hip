@@ -1,0 +1,468 @@
+// FP8 paged decode / multi-query attention for gfx950 (split-KV + reduce).
+//
+// Replaces fp8_paged_attention_decode_kernel (nanovllm/kernels/fp8_attention.py:88-171)
+// and serves the short-query (speculative decode, Lq = 1 + drafts) sequences
+// that the reference routes through fp8_paged_attention_prefill_kernel
+// (fp8_attention.py:209-312 via nanovllm/layers/attention.py:74-93).
+//
+// Work item = (sequence, kv head, KV partition).  One 256-thread workgroup
+// (4 waves) owns one item and packs every query row that reads this kv head
+// -- the G = Hq/Hkv heads times Lq query tokens -- as the 16-wide column
+// block(s) of its MFMAs, so each KV byte is fetched from HBM once.
+//
+// Per 32-token chunk a wave computes, on v_mfma_f32_16x16x32_bf16,
+//     S^T[token][col] = K[token][:] . Q[col][:]       (8 MFMAs per column block)
+//     O^T[dim][col]  += V^T[dim][token] . P^T[token][col]  (8 MFMAs per column block)
+// The FP8 cache bytes are converted to bf16 exactly with
+// v_cvt_scalef32_pk_bf16_fp8 (scale 1.0).
+//
+// Lane layouts (lane = 16*gam + r, gam in 0..3, r in 0..15):
+//   K operand : lane loads 2x16 B of token row (16j + r), bytes [16gam + 64h, +16);
+//               MFMA c = 2h+hh uses its 8 bytes [8hh, +8) as k-slots 8gam..8gam+7.
+//   Q operand : the same dims of query column (16cb + r).
+//   S^T result: lane holds tokens 16j + 4gam + i (i < 4) for column r.
+//   P^T operand: k-slot 8gam+e <-> token 4gam+e (e < 4) or 16+4gam+(e-4).
+//   V operand : lane loads 8 B (dims [8r, +8)) of each of those 8 tokens; a
+//               byte transpose (v_perm_b32) builds MFMA i's row r = dim 8r+i.
+//   O^T result: lane holds dims 32gam + 8k + i (k < 4) of column r in MFMA i.
+// Every K load instruction reads 64 contiguous bytes of 16 rows and every V
+// load instruction reads 4 whole 128-byte rows.
+//
+// Online softmax works in the log2 domain (exp2 with log2(e) folded into the
+// scale); row maxima are reduced across the 4 lane groups with two xor
+// shuffles.  At the end of a partition the 4 waves are merged through LDS.
+// A sequence that fits in one partition is normalised and written directly;
+// otherwise the partition writes (m, l, acc) and mq_reduce_kernel merges the
+// partitions with the log-sum-exp identity.
+#include "fp8_common.h"
+#include "kernels.h"
+
+namespace nvamd {
+
+namespace {
+
+constexpr int kChunk = 32;
+constexpr int kWaves = 4;
+constexpr int kPitch = kHeadDim + 4;  // LDS row pitch in floats (conflict-free 16 B writes)
+
+struct ChunkRegs {
+  u32x4 k[2][2];
+  u32x2 v[8];
+};
+
+__device__ __forceinline__ int v_token(int e, int gam) {
+  return (e < 4) ? (4 * gam + e) : (16 + 4 * gam + (e - 4));
+}
+
+__device__ __forceinline__ void load_chunk(ChunkRegs& cr, const uint8_t* __restrict__ kp,
+                                           const uint8_t* __restrict__ vp, int64_t rs,
+                                           int nvalid, int gam, int r) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int tok = 16 * j + r;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      u32x4 z = {0u, 0u, 0u, 0u};
+      if (tok < nvalid) z = *reinterpret_cast<const u32x4*>(kp + tok * rs + 16 * gam + 64 * h);
+      cr.k[j][h] = z;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int tok = v_token(e, gam);
+    u32x2 z = {0u, 0u};
+    if (tok < nvalid) z = *reinterpret_cast<const u32x2*>(vp + tok * rs + 8 * r);
+    cr.v[e] = z;
+  }
+}
+
+// 8 fp8 bytes (two dwords) -> bf16x8 (exact).
+__device__ __forceinline__ bf16x8 fp8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
+  return as_bf16x8(fp8x2_to_bf16x2<false>(lo), fp8x2_to_bf16x2<true>(lo),
+                   fp8x2_to_bf16x2<false>(hi), fp8x2_to_bf16x2<true>(hi));
+}
+
+template <int NCB>
+__device__ __forceinline__ void attend_chunk(const ChunkRegs& cr, const bf16x8 (&qop)[NCB][4],
+                                             const int (&col_limit)[NCB], int tok0, int kv_end,
+                                             float scale_log2, int gam, float (&m)[NCB],
+                                             float (&lsum)[NCB], f32x4 (&acc)[NCB][8]) {
+  // ---- S^T = K . Q^T -------------------------------------------------------
+  f32x4 s[NCB][2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    bf16x8 kop[4];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      kop[2 * h + 0] = fp8x8_to_bf16x8(cr.k[j][h].x, cr.k[j][h].y);
+      kop[2 * h + 1] = fp8x8_to_bf16x8(cr.k[j][h].z, cr.k[j][h].w);
+    }
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) {
+      f32x4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[c], qop[cb][c], a, 0, 0, 0);
+      s[cb][j] = a;
+    }
+  }
+
+  // ---- V^T operands: byte transpose of the 8 token rows -------------------
+  bf16x8 vop[8];
+  {
+    uint32_t d[8][4];  // d[i][pair] = bf16 pair (tokens 2*pair, 2*pair+1) of dim 8r+i
+#pragma unroll
+    for (int pr = 0; pr < 4; ++pr) {
+      const u32x2 x = cr.v[2 * pr], y = cr.v[2 * pr + 1];
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const uint32_t xs = half ? x.y : x.x;
+        const uint32_t ys = half ? y.y : y.x;
+        const uint32_t p01 = __builtin_amdgcn_perm(xs, ys, 0x01050004u);  // [x0 y0 x1 y1]
+        const uint32_t p23 = __builtin_amdgcn_perm(xs, ys, 0x03070206u);  // [x2 y2 x3 y3]
+        d[4 * half + 0][pr] = fp8x2_to_bf16x2<false>(p01);
+        d[4 * half + 1][pr] = fp8x2_to_bf16x2<true>(p01);
+        d[4 * half + 2][pr] = fp8x2_to_bf16x2<false>(p23);
+        d[4 * half + 3][pr] = fp8x2_to_bf16x2<true>(p23);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) vop[i] = as_bf16x8(d[i][0], d[i][1], d[i][2], d[i][3]);
+  }
+
+  // ---- online softmax + O^T += V^T . P^T -----------------------------------
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    const int lim = min(col_limit[cb], kv_end);
+    float v[2][4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int tok = tok0 + 16 * j + 4 * gam + i;
+        const float sv = (tok < lim) ? s[cb][j][i] * scale_log2 : -INFINITY;
+        v[j][i] = sv;
+        mx = fmaxf(mx, sv);
+      }
+    }
+    mx = fmaxf(mx, shfl_xor_f32(mx, 16));
+    mx = fmaxf(mx, shfl_xor_f32(mx, 32));
+    const float m_new = fmaxf(m[cb], mx);
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = exp2f(m[cb] - m_use);
+    m[cb] = m_new;
+    float ps = 0.f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[j][i] = exp2f(v[j][i] - m_use);
+        ps += v[j][i];
+      }
+    }
+    lsum[cb] = lsum[cb] * alpha + ps;
+    const bf16x8 pop = as_bf16x8(pack_bf16x2(v[0][0], v[0][1]), pack_bf16x2(v[0][2], v[0][3]),
+                                 pack_bf16x2(v[1][0], v[1][1]), pack_bf16x2(v[1][2], v[1][3]));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      acc[cb][i] *= alpha;
+      acc[cb][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop[i], pop, acc[cb][i], 0, 0, 0);
+    }
+  }
+}
+
+struct SeqGeom {
+  int row0, Lq, Lk, kv_row0;  // kv_row0: first K/V row of the sequence (contiguous layout)
+  bool active;
+};
+
+// Keys a sequence can address: at most max_parts partitions and, for the
+// paged layout, at most the block-table width (the reference's loop bound).
+__device__ __forceinline__ int key_capacity(const MqParams& p) {
+  int64_t cap = (int64_t)p.max_parts * p.part_tokens;
+  if (p.block_tables != nullptr) cap = min(cap, p.bt_stride * (int64_t)p.block_size);
+  return (int)min(cap, (int64_t)0x7fffffff);
+}
+
+__device__ __forceinline__ SeqGeom seq_geom(const MqParams& p, int seq) {
+  SeqGeom sg;
+  if (p.cu_q != nullptr) {
+    sg.row0 = p.cu_q[seq];
+    sg.Lq = p.cu_q[seq + 1] - sg.row0;
+    sg.kv_row0 = p.cu_k[seq];
+    sg.Lk = p.cu_k[seq + 1] - sg.kv_row0;
+    sg.active = sg.Lq > 0 && sg.Lq <= p.mq_max_q;
+  } else {
+    sg.row0 = seq;
+    sg.Lq = 1;
+    sg.kv_row0 = 0;
+    sg.Lk = p.context_lens[seq];
+    sg.active = true;
+  }
+  sg.Lk = min(sg.Lk, key_capacity(p));
+  return sg;
+}
+
+__device__ __forceinline__ void store_out_row8(uint16_t* __restrict__ dst, const float* o, float inv) {
+  u32x4 w;
+  w.x = out_round_bf16_bits(o[0] * inv) | (out_round_bf16_bits(o[1] * inv) << 16);
+  w.y = out_round_bf16_bits(o[2] * inv) | (out_round_bf16_bits(o[3] * inv) << 16);
+  w.z = out_round_bf16_bits(o[4] * inv) | (out_round_bf16_bits(o[5] * inv) << 16);
+  w.w = out_round_bf16_bits(o[6] * inv) | (out_round_bf16_bits(o[7] * inv) << 16);
+  *reinterpret_cast<u32x4*>(dst) = w;
+}
+
+}  // namespace
+
+template <int NCB>
+__global__ __launch_bounds__(256) void paged_mq_attn_kernel(MqParams p) {
+  __shared__ float sm_ml[kWaves][NCB * 16][2];
+  __shared__ __attribute__((aligned(16))) float sm_o[kWaves][16][kPitch];
+
+  const int part = blockIdx.x;
+  const int g = blockIdx.y;
+  const int seq = blockIdx.z;
+  const SeqGeom sg = seq_geom(p, seq);
+  if (!sg.active) return;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = wave_uniform(tid >> 6);
+  const int gam = lane >> 4, r = lane & 15;
+  const int G = p.G;
+
+  const int kv_begin = part * p.part_tokens;
+  if (sg.Lk <= 0) {
+    // Empty context (graph padding rows): the reference yields NaN here; write 0.
+    if (part == 0) {
+      for (int idx = tid; idx < sg.Lq * G * (kHeadDim / 8); idx += 256) {
+        const int col = idx / (kHeadDim / 8), d8 = idx % (kHeadDim / 8);
+        const int qi = col / G, gh = col - qi * G;
+        const int64_t row = sg.row0 + qi;
+        if (row >= p.q_rows) continue;
+        u32x4 z = {0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4*>(p.out + (row * p.Hq + g * G + gh) * kHeadDim + 8 * d8) = z;
+      }
+    }
+    return;
+  }
+  if (kv_begin >= sg.Lk) return;
+  const int kv_end = min(sg.Lk, kv_begin + p.part_tokens);
+  const int n_parts = (sg.Lk + p.part_tokens - 1) / p.part_tokens;
+
+  // ---- query operands ------------------------------------------------------
+  bf16x8 qop[NCB][4];
+  int col_limit[NCB];
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    const int col = 16 * cb + r;
+    const int qi = col / G, gh = col - qi * G;
+    const int64_t row = sg.row0 + qi;
+    const bool valid = qi < sg.Lq && row < p.q_rows;
+    col_limit[cb] = valid ? (sg.Lk - sg.Lq + qi + 1) : 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      u32x4 a = {0u, 0u, 0u, 0u}, b = {0u, 0u, 0u, 0u};
+      if (valid) {
+        const uint16_t* qp = p.q + (row * p.Hq + g * G + gh) * kHeadDim + 16 * gam + 64 * h;
+        a = *reinterpret_cast<const u32x4*>(qp);
+        b = *reinterpret_cast<const u32x4*>(qp + 8);
+      }
+      qop[cb][2 * h + 0] = as_bf16x8(a);
+      qop[cb][2 * h + 1] = as_bf16x8(b);
+    }
+  }
+
+  float m[NCB], lsum[NCB];
+  f32x4 acc[NCB][8];
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    m[cb] = -INFINITY;
+    lsum[cb] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[cb][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const int64_t rs = (int64_t)p.Hkv * kHeadDim;  // bytes between consecutive token rows
+  const int n_chunks = (kv_end - kv_begin + kChunk - 1) / kChunk;
+
+  // Resolves the K/V row pointers of chunk ci (wave-uniform).  Returns the
+  // number of valid tokens in the chunk, or 0 if its block id is invalid.
+  auto chunk_ptrs = [&](int ci, const uint8_t*& kp, const uint8_t*& vp) -> int {
+    const int t0 = kv_begin + ci * kChunk;
+    int64_t row;
+    if (p.block_tables != nullptr) {
+      const int bi = t0 / p.block_size;
+      if (bi >= p.bt_stride) return 0;
+      const int blk = wave_uniform(p.block_tables[(int64_t)seq * p.bt_stride + bi]);
+      row = (int64_t)blk * p.block_size + (t0 % p.block_size);
+      if (blk < 0 || row + kChunk > p.kv_rows) return 0;
+    } else {
+      row = (int64_t)sg.kv_row0 + t0;
+      if (row < 0 || row + min(kChunk, kv_end - t0) > p.kv_rows) return 0;
+    }
+    kp = p.k + (row * p.Hkv + g) * kHeadDim;
+    vp = p.v + (row * p.Hkv + g) * kHeadDim;
+    return min(kChunk, kv_end - t0);
+  };
+
+  ChunkRegs cur, nxt;
+  int ci = wave;
+  if (ci < n_chunks) {
+    const uint8_t *kp = p.k, *vp = p.v;
+    const int nv = chunk_ptrs(ci, kp, vp);
+    load_chunk(cur, kp, vp, rs, nv, gam, r);
+  }
+  for (; ci < n_chunks; ci += kWaves) {
+    const int cn = ci + kWaves;
+    if (cn < n_chunks) {
+      const uint8_t *kp = p.k, *vp = p.v;
+      const int nv = chunk_ptrs(cn, kp, vp);
+      load_chunk(nxt, kp, vp, rs, nv, gam, r);
+    }
+    attend_chunk<NCB>(cur, qop, col_limit, kv_begin + ci * kChunk, kv_end, p.scale_log2, gam, m,
+                      lsum, acc);
+    cur = nxt;
+  }
+
+  // ---- merge the 4 waves ---------------------------------------------------
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    lsum[cb] += shfl_xor_f32(lsum[cb], 16);
+    lsum[cb] += shfl_xor_f32(lsum[cb], 32);
+    if (gam == 0) {
+      sm_ml[wave][16 * cb + r][0] = m[cb];
+      sm_ml[wave][16 * cb + r][1] = lsum[cb];
+    }
+  }
+  __syncthreads();
+
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    {
+      const int col = 16 * cb + r;
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_ml[w][col][0]);
+      const float Ms = (M == -INFINITY) ? 0.f : M;
+      const float sc = exp2f(m[cb] - Ms);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        float* dst = &sm_o[wave][r][32 * gam + 8 * k];
+        f32x4 lo = {acc[cb][0][k] * sc, acc[cb][1][k] * sc, acc[cb][2][k] * sc, acc[cb][3][k] * sc};
+        f32x4 hi = {acc[cb][4][k] * sc, acc[cb][5][k] * sc, acc[cb][6][k] * sc, acc[cb][7][k] * sc};
+        *reinterpret_cast<f32x4*>(dst) = lo;
+        *reinterpret_cast<f32x4*>(dst + 4) = hi;
+      }
+    }
+    __syncthreads();
+    {
+      const int c16 = tid >> 4;          // column within the block
+      const int d0 = 8 * (tid & 15);     // 8 output dims
+      const int col = 16 * cb + c16;
+      const int qi = col / G, gh = col - qi * G;
+      const int64_t row = sg.row0 + qi;
+      if (qi < sg.Lq && row < p.q_rows) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_ml[w][col][0]);
+        const float Ms = (M == -INFINITY) ? 0.f : M;
+        float L = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) L += sm_ml[w][col][1] * exp2f(sm_ml[w][col][0] - Ms);
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float t = 0.f;
+#pragma unroll
+          for (int w = 0; w < kWaves; ++w) t += sm_o[w][c16][d0 + e];
+          o[e] = t;
+        }
+        const int64_t rh = row * p.Hq + g * G + gh;
+        if (n_parts == 1) {
+          const float inv = (L > 0.f) ? 1.0f / L : 0.f;
+          store_out_row8(p.out + rh * kHeadDim + d0, o, inv);
+        } else {
+          const int64_t pi = rh * p.max_parts + part;
+          float* pa = p.part_acc + pi * kHeadDim + d0;
+          *reinterpret_cast<f32x4*>(pa) = f32x4{o[0], o[1], o[2], o[3]};
+          *reinterpret_cast<f32x4*>(pa + 4) = f32x4{o[4], o[5], o[6], o[7]};
+          if (d0 == 0) {
+            p.part_ml[2 * pi + 0] = M;
+            p.part_ml[2 * pi + 1] = L;
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// One wave per (query row, head): log-sum-exp merge of the partitions.
+__global__ __launch_bounds__(256) void mq_reduce_kernel(MqParams p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t rh = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (rh >= p.q_rows * p.Hq) return;
+  const int64_t row = rh / p.Hq;
+  int Lk;
+  if (p.cu_q != nullptr) {
+    // sequence owning this row: largest s with cu_q[s] <= row
+    int lo = 0, hi = p.num_seqs;  // invariant: cu_q[lo] <= row < cu_q[hi]
+    if (row >= p.cu_q[p.num_seqs] || row < p.cu_q[0]) return;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (p.cu_q[mid] <= row) lo = mid; else hi = mid;
+    }
+    const int Lq = p.cu_q[lo + 1] - p.cu_q[lo];
+    if (Lq <= 0 || Lq > p.mq_max_q) return;
+    Lk = p.cu_k[lo + 1] - p.cu_k[lo];
+  } else {
+    if (row >= p.num_seqs) return;
+    Lk = p.context_lens[row];
+  }
+  Lk = min(Lk, key_capacity(p));
+  if (Lk <= 0) return;
+  const int n_parts = (Lk + p.part_tokens - 1) / p.part_tokens;
+  if (n_parts <= 1) return;
+
+  const float* ml = p.part_ml + 2 * rh * p.max_parts;
+  float M = -INFINITY;
+  for (int q = lane; q < n_parts; q += 64) M = fmaxf(M, ml[2 * q]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, shfl_xor_f32(M, off));
+  const float Ms = (M == -INFINITY) ? 0.f : M;
+  float L = 0.f;
+  for (int q = lane; q < n_parts; q += 64) L += ml[2 * q + 1] * exp2f(ml[2 * q] - Ms);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) L += shfl_xor_f32(L, off);
+
+  const float* pa = p.part_acc + rh * p.max_parts * kHeadDim + 2 * lane;
+  float o0 = 0.f, o1 = 0.f;
+  for (int q = 0; q < n_parts; ++q) {
+    const float w = exp2f(ml[2 * q] - Ms);
+    const f32x2 a = *reinterpret_cast<const f32x2*>(pa + (int64_t)q * kHeadDim);
+    o0 += w * a.x;
+    o1 += w * a.y;
+  }
+  const float inv = (L > 0.f) ? 1.0f / L : 0.f;
+  const uint32_t w = out_round_bf16_bits(o0 * inv) | (out_round_bf16_bits(o1 * inv) << 16);
+  *reinterpret_cast<uint32_t*>(p.out + rh * kHeadDim + 2 * lane) = w;
+}
+
+hipError_t launch_paged_mq(const MqParams& p, int ncb, hipStream_t stream) {
+  if (p.num_seqs == 0) return hipSuccess;
+  const dim3 grid((unsigned)p.max_parts, (unsigned)p.Hkv, (unsigned)p.num_seqs);
+  switch (ncb) {
+    case 1: hipLaunchKernelGGL(paged_mq_attn_kernel<1>, grid, dim3(256), 0, stream, p); break;
+    case 2: hipLaunchKernelGGL(paged_mq_attn_kernel<2>, grid, dim3(256), 0, stream, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (p.max_parts > 1) {
+    const int64_t waves = p.q_rows * p.Hq;
+    hipLaunchKernelGGL(mq_reduce_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream, p);
+    e = hipGetLastError();
+  }
+  return e;
+}
+
+}  // namespace nvamd

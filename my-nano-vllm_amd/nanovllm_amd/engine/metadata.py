@@ -1,0 +1,140 @@
+"""Host-side attention metadata: slot mapping, cu_seqlens, context lengths, block tables.
+
+Behaviour of nanovllm/engine/model_runner.py:133-220, built per sequence with
+numpy instead of per-token Python loops, then copied to the GPU from pinned
+memory with non-blocking copies (as the reference does, :141, :183-184,
+:199, :211-213):
+
+* plain decode sequences (``num_scheduled_tokens == 1``, :205):
+  ``position = len - 1``, ``context_len = len`` and
+  ``slot = block_table[-1] * bs + last_block_num_tokens - 1`` (:195-198);
+* varlen sequences (speculative-decode rows first, then prefill chunks,
+  :206-209): query positions ``[num_cached, num_cached + num_scheduled)``,
+  ``cu_seqlens_q`` / ``cu_seqlens_k`` prefix sums of ``num_scheduled`` and of
+  ``num_cached + num_scheduled`` (:166-167) and, for every scheduled position
+  p, ``slot = block_table[p // bs] * bs + p % bs`` (the block walk of
+  :172-182); a sequence without a block table contributes no slots (:170);
+* block tables in [plain decode | speculative | prefill] order, padded with
+  -1 to the longest table (:133-142, :216).
+
+``Seq``-like inputs need ``len(seq)``, ``num_cached_tokens``,
+``num_scheduled_tokens`` and ``block_table`` -- nano-vLLM's ``Sequence``
+qualifies.
+"""
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from ..utils.context import set_context
+
+
+def _seq_len(seq):
+    return len(seq) if hasattr(seq, "__len__") else int(seq.num_tokens)
+
+
+@dataclass
+class HostMetadata:
+    """Host (numpy) form of one step's attention metadata."""
+    positions: np.ndarray          # int64 [num_tokens]
+    slot_mapping: np.ndarray       # int32 [num_tokens]
+    context_lens: np.ndarray       # int32 [num_plain_decode]
+    cu_seqlens_q: np.ndarray       # int32 [num_varlen + 1] (empty if no varlen rows)
+    cu_seqlens_k: np.ndarray
+    max_seqlen_q: int
+    max_seqlen_k: int
+    block_tables: np.ndarray       # int32 [num_seqs_with_tables, max_len] (-1 padded) or None
+    split_pt: int
+    num_spec_seqs: int
+
+
+def decode_rows(seqs, block_size):
+    n = len(seqs)
+    lens = np.fromiter((_seq_len(s) for s in seqs), dtype=np.int64, count=n)
+    last_blk = np.fromiter((s.block_table[-1] for s in seqs), dtype=np.int64, count=n)
+    num_blocks = (lens + block_size - 1) // block_size
+    last_block_tokens = lens - (num_blocks - 1) * block_size
+    slots = last_blk * block_size + last_block_tokens - 1
+    return lens - 1, slots.astype(np.int32), lens.astype(np.int32)
+
+
+def varlen_rows(seqs, block_size):
+    starts = np.array([s.num_cached_tokens for s in seqs], dtype=np.int64)
+    lq = np.array([s.num_scheduled_tokens for s in seqs], dtype=np.int64)
+    ends = starts + lq
+    cu_q = np.zeros(len(seqs) + 1, dtype=np.int64)
+    cu_k = np.zeros(len(seqs) + 1, dtype=np.int64)
+    np.cumsum(lq, out=cu_q[1:])
+    np.cumsum(ends, out=cu_k[1:])
+    positions = np.concatenate([np.arange(a, b, dtype=np.int64) for a, b in zip(starts, ends)]) \
+        if len(seqs) else np.zeros(0, dtype=np.int64)
+    slot_parts = []
+    for s, a, b in zip(seqs, starts, ends):
+        if not s.block_table:
+            continue
+        pos = np.arange(a, b, dtype=np.int64)
+        table = np.asarray(s.block_table, dtype=np.int64)
+        slot_parts.append(table[pos // block_size] * block_size + pos % block_size)
+    slots = np.concatenate(slot_parts).astype(np.int32) if slot_parts else np.zeros(0, dtype=np.int32)
+    max_q = int(lq.max()) if len(seqs) else 0
+    max_k = int(ends.max()) if len(seqs) else 0
+    return positions, slots, cu_q.astype(np.int32), cu_k.astype(np.int32), max_q, max_k
+
+
+def padded_block_tables(seqs):
+    tables = [s.block_table for s in seqs if s.block_table]
+    if not tables:
+        return None
+    width = max(len(t) for t in tables)
+    out = np.full((len(tables), width), -1, dtype=np.int32)
+    for i, t in enumerate(tables):
+        out[i, :len(t)] = t
+    return out
+
+
+def build_host_metadata(dseqs, pseqs, block_size) -> HostMetadata:
+    nd = [s for s in dseqs if s.num_scheduled_tokens == 1]
+    sd = [s for s in dseqs if s.num_scheduled_tokens > 1]
+    varlen = sd + list(pseqs)
+    if nd:
+        dpos, dslot, ctx = decode_rows(nd, block_size)
+    else:
+        dpos, dslot, ctx = (np.zeros(0, np.int64), np.zeros(0, np.int32), np.zeros(0, np.int32))
+    if varlen:
+        ppos, pslot, cu_q, cu_k, max_q, max_k = varlen_rows(varlen, block_size)
+    else:
+        ppos, pslot = np.zeros(0, np.int64), np.zeros(0, np.int32)
+        cu_q = cu_k = np.zeros(0, np.int32)
+        max_q = max_k = 0
+    return HostMetadata(
+        positions=np.concatenate([dpos, ppos]),
+        slot_mapping=np.concatenate([dslot, pslot]).astype(np.int32),
+        context_lens=ctx, cu_seqlens_q=cu_q, cu_seqlens_k=cu_k,
+        max_seqlen_q=max_q, max_seqlen_k=max_k,
+        block_tables=padded_block_tables(nd + sd + list(pseqs)),
+        split_pt=len(nd), num_spec_seqs=len(sd))
+
+
+def _to_device(arr, device):
+    if arr is None:
+        return None
+    t = torch.from_numpy(np.ascontiguousarray(arr))
+    if torch.device(device).type == "cuda":
+        return t.pin_memory().to(device, non_blocking=True)
+    return t.to(device)
+
+
+def prepare_sequence(dseqs, pseqs, block_size, device="cuda"):
+    """Builds the step's metadata, publishes it through the Context and returns
+    the device positions (model_runner.prepare_sequence, :203-220)."""
+    md = build_host_metadata(dseqs, pseqs, block_size)
+    has_varlen = md.cu_seqlens_q.size > 0
+    set_context(
+        split_pt=md.split_pt, num_spec_seqs=md.num_spec_seqs,
+        slot_mapping=_to_device(md.slot_mapping, device),
+        context_lens=_to_device(md.context_lens, device) if md.split_pt else None,
+        cu_seqlens_q=_to_device(md.cu_seqlens_q, device) if has_varlen else None,
+        cu_seqlens_k=_to_device(md.cu_seqlens_k, device) if has_varlen else None,
+        max_seqlen_q=md.max_seqlen_q, max_seqlen_k=md.max_seqlen_k,
+        block_tables=_to_device(md.block_tables, device))
+    return _to_device(md.positions, device)

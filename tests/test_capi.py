@@ -1,0 +1,48 @@
+"""The C-ABI library loads, exports every symbol the public header declares,
+and rejects bad arguments before touching the GPU (host logic only)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from nanovllm_amd import _native
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "nvamd_fp8_attention.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(nvamd_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points():
+    assert _declared() == sorted(_native.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.load()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.nvamd_abi_version() == _native.ABI_VERSION
+
+
+def test_rejects_unsupported_head_dim_without_gpu():
+    lib = _native.load()
+    st = lib.nvamd_fp8_decode_attention(None, None, None, None, None, None, 4, 8, 2, 64, 16, 256, 4,
+                                        0.1, 0, None, 0, None)
+    assert st == 2
+    assert b"head_dim" in lib.nvamd_last_error()
+
+
+def test_rejects_bad_gqa_and_block_size_without_gpu():
+    lib = _native.load()
+    assert lib.nvamd_fp8_decode_attention(None, None, None, None, None, None, 4, 6, 4, 128, 16, 256, 4,
+                                          0.1, 0, None, 0, None) == 1
+    assert lib.nvamd_fp8_decode_attention(None, None, None, None, None, None, 4, 8, 2, 128, 16, 48, 4,
+                                          0.1, 0, None, 0, None) == 2
+    assert lib.nvamd_fp8_prefill_attention(None, None, None, None, None, None, None, 4, 1, 8, 2, 128, 100,
+                                           256, 2, 4, 4, 0.1, 100, None, 0, None) == 1  # part_tokens % 256
+    assert b"part_tokens" in lib.nvamd_last_error()
+    assert lib.nvamd_store_kvcache(None, 0, None, 0, None, None, None, -1, 8, 128, 10, None) == 1

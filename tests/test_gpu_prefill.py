@@ -1,0 +1,94 @@
+"""Varlen causal (chunked) FP8 prefill on the GPU vs the oracle, paged and contiguous."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import announce, assert_close, build_pair
+from oracle import attention as oa
+from nanovllm_amd import workloads as W
+from nanovllm_amd.kernels.fp8_attention import fp8_decode_attention, fp8_prefill_attention
+
+pytestmark = pytest.mark.gpu
+SCALE = 128 ** -0.5
+
+
+def _prefill_gpu(wl, gpu_c, q, paged=True, kv=None, cu_k=None):
+    cu_q, cu_k_p = wl.cu_seqlens()
+    kw = dict(cu_seqlens_q=torch.from_numpy(cu_q).cuda(),
+              cu_seqlens_k=torch.from_numpy(cu_k_p if cu_k is None else cu_k).cuda(),
+              max_seqlen_q=int(wl.lq().max()), max_seqlen_k=int(wl.lk().max()), softmax_scale=SCALE)
+    if paged:
+        out = fp8_prefill_attention(q, gpu_c[0], gpu_c[1], block_tables=torch.from_numpy(wl.block_tables).cuda(), **kw)
+    else:
+        out = fp8_prefill_attention(q, kv[0], kv[1], block_tables=None, **kw)
+    torch.cuda.synchronize()
+    return out
+
+
+def _prefill_oracle(wl, cpu_c, q):
+    cu_q, cu_k = wl.cu_seqlens()
+    return oa.prefill_attention(q, cpu_c[0], cpu_c[1], torch.from_numpy(wl.block_tables),
+                                torch.from_numpy(cu_q), torch.from_numpy(cu_k), SCALE)
+
+
+def _check(wl):
+    cpu_c, gpu_c = build_pair(wl)
+    q = wl.make_q("cpu")
+    out = _prefill_gpu(wl, gpu_c, q.cuda())
+    assert_close(out, _prefill_oracle(wl, cpu_c, q), wl.name)
+    return cpu_c, gpu_c, q, out
+
+
+def test_prefill_qwen3_8b_chunks():
+    wl = W.qwen3_8b_prefill()
+    announce(f"prefill: {wl.name}")
+    _check(wl)
+
+
+def test_prefill_mixed_spec_and_chunks():
+    full = W.qwen3_8b_mixed()
+    wl = W.sub_workload(full, range(192, full.num_seqs), name="mixed_varlen")  # spec + chunks
+    announce(f"prefill: {wl.name} (32 spec x 5 + 3 x 512)")
+    _check(wl)
+
+
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (16, 8), (64, 8), (8, 8), (24, 8)])
+def test_prefill_ragged(hq, hkv):
+    rng = np.random.default_rng(hq + 7 * hkv)
+    lqs = [1, 2, 3, 5, 8, 9, 17, 31, 32, 33, 64, 100, 129, 300]
+    seqs = [W.SeqSpec(lq=int(l), cached=int(rng.integers(0, 700))) for l in lqs]
+    seqs.append(W.SeqSpec(lq=77, cached=0))
+    wl = W.make_workload(f"ragged_{hq}_{hkv}", hq, hkv, seqs, seed=int(rng.integers(1 << 30)))
+    announce(f"prefill: ragged GQA {hq}/{hkv}")
+    _check(wl)
+
+
+def test_prefill_contiguous_equals_paged():
+    rng = np.random.default_rng(3)
+    seqs = [W.SeqSpec(lq=l, cached=0) for l in (1024, 300, 65, 4)]
+    wl = W.make_workload("contiguous_prompts", 32, 8, seqs, seed=99)
+    announce("prefill: contiguous layout (block_tables=None)")
+    cpu_c, gpu_c, q, paged_out = _check(wl)
+    # gather each sequence's K/V rows out of the paged cache into [Nk, Hkv, D]
+    bt = wl.block_tables
+    rows = np.concatenate([wl.slots_for(i, 0, s.lk) for i, s in enumerate(wl.seqs)]).astype(np.int64)
+    idx = torch.from_numpy(rows).cuda()
+    kcont = gpu_c[0].view(torch.uint8).reshape(-1, 8, 128)[idx].view(torch.float8_e4m3fn)
+    vcont = gpu_c[1].view(torch.uint8).reshape(-1, 8, 128)[idx].view(torch.float8_e4m3fn)
+    out = _prefill_gpu(wl, gpu_c, q.cuda(), paged=False, kv=(kcont, vcont))
+    cu_q, cu_k = wl.cu_seqlens()
+    want = oa.prefill_attention(q, kcont.cpu(), vcont.cpu(), None, torch.from_numpy(cu_q),
+                                torch.from_numpy(cu_k), SCALE)
+    assert_close(out, want, "contiguous")
+    assert_close(out, paged_out, "contiguous vs paged", atol=1e-3, rtol=1e-3)
+
+
+def test_prefill_lq1_equals_decode():
+    announce("prefill: Lq=1 rows equal decode")
+    wl = W.qwen3_0p6b_decode(B=24)
+    _, gpu_c = build_pair(wl)
+    q = wl.make_q("cuda")
+    dec = fp8_decode_attention(q, gpu_c[0], gpu_c[1], torch.from_numpy(wl.block_tables).cuda(),
+                               torch.from_numpy(wl.context_lens()).cuda(), SCALE)
+    pre = _prefill_gpu(wl, gpu_c, q)
+    assert torch.equal(dec, pre)
