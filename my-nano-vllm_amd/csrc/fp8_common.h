@@ -21,6 +21,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kHeadDim = 128;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -63,15 +64,23 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
   return __builtin_bit_cast(float, bits16 << 16);
 }
 
-// fp32 -> bf16 bits, round to nearest even (finite inputs).
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __builtin_bit_cast(uint32_t, f);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return u >> 16;
+// Two fp32 -> two bf16 (round to nearest even) in one dword: v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+// 2**x with the bare v_exp_f32 (inputs here are <= 0 or -inf; tiny results
+// may flush to zero, which is harmless for softmax weights).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Online softmax keeps a reference maximum per row and only rescales the
+// accumulators when a new score exceeds it by more than this many powers of
+// two; in between, weights exp2(s - m_ref) stay below 2**8.
+constexpr float kLazyRescaleLog2 = 8.0f;
+
+__device__ __forceinline__ bool wave_any(bool pred) {
+  return __builtin_amdgcn_ballot_w64(pred) != 0;
 }
 
 // The reference stores fp16(acc / l) into a bf16 tensor: fp32 -> fp16 (RNE)
@@ -95,6 +104,27 @@ __device__ __forceinline__ float shfl_xor_f32(float v, int mask) {
 
 __device__ __forceinline__ int wave_uniform(int v) {
   return __builtin_amdgcn_readfirstlane(v);
+}
+
+// ---------------------------------------------------------------------------
+// Raw buffer loads: the descriptor's num_records bounds every access, and
+// bytes at or past it read as zero (no exec-masked branches around loads).
+// All offsets go in the VGPR offset (soffset = 0) so the range check sees them.
+// ---------------------------------------------------------------------------
+
+constexpr int kBufferRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t num_bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)num_bytes,
+                                           kBufferRsrcWord3);
+}
+
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+__device__ __forceinline__ u32x2 buf_load8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
 }
 
 // bf16x8 from four packed dwords.

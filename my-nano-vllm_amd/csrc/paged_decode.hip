@@ -10,27 +10,30 @@
 // -- the G = Hq/Hkv heads times Lq query tokens -- as the 16-wide column
 // block(s) of its MFMAs, so each KV byte is fetched from HBM once.
 //
-// Per 32-token chunk a wave computes, on v_mfma_f32_16x16x32_bf16,
-//     S^T[token][col] = K[token][:] . Q[col][:]       (8 MFMAs per column block)
-//     O^T[dim][col]  += V^T[dim][token] . P^T[token][col]  (8 MFMAs per column block)
+// Per 16-token chunk a wave computes, in fp32 accumulators:
+//     S^T[token][col] = K[token][:] . Q[col][:]      4 x v_mfma_f32_16x16x32_bf16 per column block
+//     O^T[dim][col]  += V^T[dim][token] . P^T[token][col]   8 x v_mfma_f32_16x16x16_bf16
 // The FP8 cache bytes are converted to bf16 exactly with
 // v_cvt_scalef32_pk_bf16_fp8 (scale 1.0).
 //
 // Lane layouts (lane = 16*gam + r, gam in 0..3, r in 0..15):
-//   K operand : lane loads 2x16 B of token row (16j + r), bytes [16gam + 64h, +16);
+//   K operand : lane loads 2x16 B of token row r, bytes [16gam + 64h, +16);
 //               MFMA c = 2h+hh uses its 8 bytes [8hh, +8) as k-slots 8gam..8gam+7.
 //   Q operand : the same dims of query column (16cb + r).
-//   S^T result: lane holds tokens 16j + 4gam + i (i < 4) for column r.
-//   P^T operand: k-slot 8gam+e <-> token 4gam+e (e < 4) or 16+4gam+(e-4).
-//   V operand : lane loads 8 B (dims [8r, +8)) of each of those 8 tokens; a
-//               byte transpose (v_perm_b32) builds MFMA i's row r = dim 8r+i.
+//   S^T result: lane holds tokens 4gam + i (i < 4) for column r -- which is
+//               exactly the k-slot layout of the 16x16x16 B operand, so P^T
+//               needs no data movement.
+//   V operand : lane loads 8 B (dims [8r, +8)) of tokens 4gam..4gam+3; a byte
+//               transpose (v_perm_b32) builds MFMA i's row r = dim 8r+i.
 //   O^T result: lane holds dims 32gam + 8k + i (k < 4) of column r in MFMA i.
 // Every K load instruction reads 64 contiguous bytes of 16 rows and every V
-// load instruction reads 4 whole 128-byte rows.
+// load instruction reads 4 whole 128-byte rows.  Loads are raw buffer loads
+// whose descriptor bounds the chunk's valid rows (rows past the end read 0).
+// Three chunks are in flight per wave (triple-buffered registers).
 //
 // Online softmax works in the log2 domain (exp2 with log2(e) folded into the
-// scale); row maxima are reduced across the 4 lane groups with two xor
-// shuffles.  At the end of a partition the 4 waves are merged through LDS.
+// scale); row maxima are reduced across the 4 lane groups with the gfx950
+// v_permlane16_swap / v_permlane32_swap exchanges (no LDS traffic).  At the end of a partition the 4 waves are merged through LDS.
 // A sequence that fits in one partition is normalised and written directly;
 // otherwise the partition writes (m, l, acc) and mq_reduce_kernel merges the
 // partitions with the log-sum-exp identity.
@@ -41,39 +44,22 @@ namespace nvamd {
 
 namespace {
 
-constexpr int kChunk = 32;
+constexpr int kChunk = 16;
 constexpr int kWaves = 4;
 constexpr int kPitch = kHeadDim + 4;  // LDS row pitch in floats (conflict-free 16 B writes)
 
 struct ChunkRegs {
-  u32x4 k[2][2];
-  u32x2 v[8];
+  u32x4 k[2];   // K row r, bytes [16gam + 64h, +16)
+  u32x2 v[4];   // V rows 4gam + e, bytes [8r, +8)
 };
 
-__device__ __forceinline__ int v_token(int e, int gam) {
-  return (e < 4) ? (4 * gam + e) : (16 + 4 * gam + (e - 4));
-}
-
-__device__ __forceinline__ void load_chunk(ChunkRegs& cr, const uint8_t* __restrict__ kp,
-                                           const uint8_t* __restrict__ vp, int64_t rs,
-                                           int nvalid, int gam, int r) {
+__device__ __forceinline__ void load_chunk(ChunkRegs& cr, __amdgpu_buffer_rsrc_t rk,
+                                           __amdgpu_buffer_rsrc_t rv, uint32_t k_off,
+                                           uint32_t v_off, uint32_t rs) {
+  cr.k[0] = buf_load16(rk, k_off);
+  cr.k[1] = buf_load16(rk, k_off + 64u);
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int tok = 16 * j + r;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      u32x4 z = {0u, 0u, 0u, 0u};
-      if (tok < nvalid) z = *reinterpret_cast<const u32x4*>(kp + tok * rs + 16 * gam + 64 * h);
-      cr.k[j][h] = z;
-    }
-  }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int tok = v_token(e, gam);
-    u32x2 z = {0u, 0u};
-    if (tok < nvalid) z = *reinterpret_cast<const u32x2*>(vp + tok * rs + 8 * r);
-    cr.v[e] = z;
-  }
+  for (int e = 0; e < 4; ++e) cr.v[e] = buf_load8(rv, v_off + (uint32_t)e * rs);
 }
 
 // 8 fp8 bytes (two dwords) -> bf16x8 (exact).
@@ -82,92 +68,99 @@ __device__ __forceinline__ bf16x8 fp8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
                    fp8x2_to_bf16x2<false>(hi), fp8x2_to_bf16x2<true>(hi));
 }
 
+__device__ __forceinline__ s16x4 as_s16x4(uint32_t a, uint32_t b) {
+  u32x2 t = {a, b};
+  return __builtin_bit_cast(s16x4, t);
+}
+
+// max over the 4 lanes {l, l^16, l^32, l^48} (the lane groups holding one
+// column), with the gfx950 row-swap exchanges: permlane16/32_swap(x, x)
+// leaves each lane holding {x[l], x[l^16]} (resp. x[l^32]) across its two
+// results.  The results are copied to scalars before the bit cast:
+// __builtin_bit_cast of an ext-vector element lvalue reads element 0.
+__device__ __forceinline__ float pair_max(uint32_t lo, uint32_t hi) {
+  return fmaxf(__builtin_bit_cast(float, lo), __builtin_bit_cast(float, hi));
+}
+
+__device__ __forceinline__ float col_max(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const uint32_t a0 = a[0], a1 = a[1];
+  const uint32_t w = __builtin_bit_cast(uint32_t, pair_max(a0, a1));
+  const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+  const uint32_t b0 = b[0], b1 = b[1];
+  return pair_max(b0, b1);
+}
+
 template <int NCB>
 __device__ __forceinline__ void attend_chunk(const ChunkRegs& cr, const bf16x8 (&qop)[NCB][4],
-                                             const int (&col_limit)[NCB], int tok0, int kv_end,
+                                             const int (&col_limit)[NCB], int tok0, bool need_mask,
                                              float scale_log2, int gam, float (&m)[NCB],
                                              float (&lsum)[NCB], f32x4 (&acc)[NCB][8]) {
   // ---- S^T = K . Q^T -------------------------------------------------------
-  f32x4 s[NCB][2];
+  bf16x8 kop[4];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    bf16x8 kop[4];
+  for (int h = 0; h < 2; ++h) {
+    kop[2 * h + 0] = fp8x8_to_bf16x8(cr.k[h].x, cr.k[h].y);
+    kop[2 * h + 1] = fp8x8_to_bf16x8(cr.k[h].z, cr.k[h].w);
+  }
+  f32x4 s[NCB];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      kop[2 * h + 0] = fp8x8_to_bf16x8(cr.k[j][h].x, cr.k[j][h].y);
-      kop[2 * h + 1] = fp8x8_to_bf16x8(cr.k[j][h].z, cr.k[j][h].w);
-    }
+  for (int cb = 0; cb < NCB; ++cb) {
+    f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int cb = 0; cb < NCB; ++cb) {
-      f32x4 a = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int c = 0; c < 4; ++c) a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[c], qop[cb][c], a, 0, 0, 0);
-      s[cb][j] = a;
-    }
+    for (int c = 0; c < 4; ++c) a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[c], qop[cb][c], a, 0, 0, 0);
+    s[cb] = a;
   }
 
-  // ---- V^T operands: byte transpose of the 8 token rows -------------------
-  bf16x8 vop[8];
-  {
-    uint32_t d[8][4];  // d[i][pair] = bf16 pair (tokens 2*pair, 2*pair+1) of dim 8r+i
+  // ---- V^T operands: byte transpose of the 4 token rows --------------------
+  s16x4 vop[8];
 #pragma unroll
-    for (int pr = 0; pr < 4; ++pr) {
-      const u32x2 x = cr.v[2 * pr], y = cr.v[2 * pr + 1];
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const uint32_t xs = half ? x.y : x.x;
-        const uint32_t ys = half ? y.y : y.x;
-        const uint32_t p01 = __builtin_amdgcn_perm(xs, ys, 0x01050004u);  // [x0 y0 x1 y1]
-        const uint32_t p23 = __builtin_amdgcn_perm(xs, ys, 0x03070206u);  // [x2 y2 x3 y3]
-        d[4 * half + 0][pr] = fp8x2_to_bf16x2<false>(p01);
-        d[4 * half + 1][pr] = fp8x2_to_bf16x2<true>(p01);
-        d[4 * half + 2][pr] = fp8x2_to_bf16x2<false>(p23);
-        d[4 * half + 3][pr] = fp8x2_to_bf16x2<true>(p23);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) vop[i] = as_bf16x8(d[i][0], d[i][1], d[i][2], d[i][3]);
+  for (int half = 0; half < 2; ++half) {
+    const uint32_t x0 = half ? cr.v[0].y : cr.v[0].x;
+    const uint32_t x1 = half ? cr.v[1].y : cr.v[1].x;
+    const uint32_t x2 = half ? cr.v[2].y : cr.v[2].x;
+    const uint32_t x3 = half ? cr.v[3].y : cr.v[3].x;
+    const uint32_t a01 = __builtin_amdgcn_perm(x0, x1, 0x01050004u);  // [t0d0 t1d0 t0d1 t1d1]
+    const uint32_t b01 = __builtin_amdgcn_perm(x0, x1, 0x03070206u);  // [t0d2 t1d2 t0d3 t1d3]
+    const uint32_t a23 = __builtin_amdgcn_perm(x2, x3, 0x01050004u);
+    const uint32_t b23 = __builtin_amdgcn_perm(x2, x3, 0x03070206u);
+    vop[4 * half + 0] = as_s16x4(fp8x2_to_bf16x2<false>(a01), fp8x2_to_bf16x2<false>(a23));
+    vop[4 * half + 1] = as_s16x4(fp8x2_to_bf16x2<true>(a01), fp8x2_to_bf16x2<true>(a23));
+    vop[4 * half + 2] = as_s16x4(fp8x2_to_bf16x2<false>(b01), fp8x2_to_bf16x2<false>(b23));
+    vop[4 * half + 3] = as_s16x4(fp8x2_to_bf16x2<true>(b01), fp8x2_to_bf16x2<true>(b23));
   }
 
   // ---- online softmax + O^T += V^T . P^T -----------------------------------
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) {
-    const int lim = min(col_limit[cb], kv_end);
-    float v[2][4];
-    float mx = -INFINITY;
+    float v[4];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int i = 0; i < 4; ++i) v[i] = s[cb][i] * scale_log2;
+    if (need_mask) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int tok = tok0 + 16 * j + 4 * gam + i;
-        const float sv = (tok < lim) ? s[cb][j][i] * scale_log2 : -INFINITY;
-        v[j][i] = sv;
-        mx = fmaxf(mx, sv);
-      }
+      for (int i = 0; i < 4; ++i) v[i] = (tok0 + 4 * gam + i < col_limit[cb]) ? v[i] : -INFINITY;
     }
-    mx = fmaxf(mx, shfl_xor_f32(mx, 16));
-    mx = fmaxf(mx, shfl_xor_f32(mx, 32));
-    const float m_new = fmaxf(m[cb], mx);
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = exp2f(m[cb] - m_use);
-    m[cb] = m_new;
-    float ps = 0.f;
+    const float mx = col_max(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+    // Lazy rescale: move the reference max only when a score exceeds it by
+    // more than 2**kLazyRescaleLog2 (always on a column's first valid chunk).
+    const bool grow = mx > m[cb] + kLazyRescaleLog2;
+    if (wave_any(grow)) {
+      const float m_new = grow ? mx : m[cb];
+      const float alpha = grow ? fast_exp2(m[cb] - m_new) : 1.f;
+      m[cb] = m_new;
+      lsum[cb] *= alpha;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v[j][i] = exp2f(v[j][i] - m_use);
-        ps += v[j][i];
-      }
+      for (int i = 0; i < 8; ++i) acc[cb][i] *= alpha;
     }
-    lsum[cb] = lsum[cb] * alpha + ps;
-    const bf16x8 pop = as_bf16x8(pack_bf16x2(v[0][0], v[0][1]), pack_bf16x2(v[0][2], v[0][3]),
-                                 pack_bf16x2(v[1][0], v[1][1]), pack_bf16x2(v[1][2], v[1][3]));
+    const float m_use = (m[cb] == -INFINITY) ? 0.f : m[cb];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      acc[cb][i] *= alpha;
-      acc[cb][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop[i], pop, acc[cb][i], 0, 0, 0);
-    }
+    for (int i = 0; i < 4; ++i) v[i] = fast_exp2(v[i] - m_use);
+    lsum[cb] += (v[0] + v[1]) + (v[2] + v[3]);
+    const s16x4 pop = as_s16x4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      acc[cb][i] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vop[i], pop, acc[cb][i], 0, 0, 0);
   }
 }
 
@@ -284,49 +277,68 @@ __global__ __launch_bounds__(256) void paged_mq_attn_kernel(MqParams p) {
   const int64_t rs = (int64_t)p.Hkv * kHeadDim;  // bytes between consecutive token rows
   const int n_chunks = (kv_end - kv_begin + kChunk - 1) / kChunk;
 
-  // Resolves the K/V row pointers of chunk ci (wave-uniform).  Returns the
-  // number of valid tokens in the chunk, or 0 if its block id is invalid.
-  auto chunk_ptrs = [&](int ci, const uint8_t*& kp, const uint8_t*& vp) -> int {
+  // Buffer descriptors of chunk ci (wave-uniform), bounded to its valid rows.
+  // A chunk (32 tokens) never straddles a KV block (block_size % 64 == 0).
+  // Chunks past the partition get num_records = 0: their loads are still
+  // issued (so every loop path has the same number of loads in flight and
+  // the wait counts stay exact) but read nothing and return zeros.
+  auto chunk_rsrc = [&](int ci, __amdgpu_buffer_rsrc_t& rk, __amdgpu_buffer_rsrc_t& rv) {
     const int t0 = kv_begin + ci * kChunk;
-    int64_t row;
+    int nvalid = max(0, min(kChunk, kv_end - t0));
+    int64_t row = 0;
     if (p.block_tables != nullptr) {
-      const int bi = t0 / p.block_size;
-      if (bi >= p.bt_stride) return 0;
+      const int bi = min(t0 / p.block_size, (int)p.bt_stride - 1);
       const int blk = wave_uniform(p.block_tables[(int64_t)seq * p.bt_stride + bi]);
       row = (int64_t)blk * p.block_size + (t0 % p.block_size);
-      if (blk < 0 || row + kChunk > p.kv_rows) return 0;
+      if (blk < 0 || row + kChunk > p.kv_rows) nvalid = 0;
     } else {
       row = (int64_t)sg.kv_row0 + t0;
-      if (row < 0 || row + min(kChunk, kv_end - t0) > p.kv_rows) return 0;
+      if (row < 0 || row + nvalid > p.kv_rows) nvalid = 0;
     }
-    kp = p.k + (row * p.Hkv + g) * kHeadDim;
-    vp = p.v + (row * p.Hkv + g) * kHeadDim;
-    return min(kChunk, kv_end - t0);
+    if (nvalid == 0) row = 0;
+    const int64_t base = (row * p.Hkv + g) * kHeadDim;
+    rk = make_rsrc(p.k + base, (uint32_t)(nvalid * rs));
+    rv = make_rsrc(p.v + base, (uint32_t)(nvalid * rs));
   };
 
-  ChunkRegs cur, nxt;
+  const uint32_t urs = (uint32_t)rs;
+  const uint32_t k_off = (uint32_t)r * urs + 16u * gam;
+  const uint32_t v_off = 4u * gam * urs + 8u * r;
+  // Masking is needed only on chunks that reach past the smallest visible
+  // limit of any column (or past the partition end, whose rows read as 0).
+  const int mask_from = min(kv_end, sg.Lk - sg.Lq + 1);
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) col_limit[cb] = min(col_limit[cb], kv_end);
+
+  // Three register buffers in rotation, all always in flight: while one
+  // chunk is computed the next two are loading.  Every path into the loop
+  // head has the same loads outstanding, so each compute waits only for its
+  // own buffer.
+  ChunkRegs buf[3];
+  __amdgpu_buffer_rsrc_t rk, rv;
   int ci = wave;
-  if (ci < n_chunks) {
-    const uint8_t *kp = p.k, *vp = p.v;
-    const int nv = chunk_ptrs(ci, kp, vp);
-    load_chunk(cur, kp, vp, rs, nv, gam, r);
+#pragma unroll
+  for (int b = 0; b < 3; ++b) {
+    chunk_rsrc(ci + b * kWaves, rk, rv);
+    load_chunk(buf[b], rk, rv, k_off, v_off, urs);
   }
-  for (; ci < n_chunks; ci += kWaves) {
-    const int cn = ci + kWaves;
-    if (cn < n_chunks) {
-      const uint8_t *kp = p.k, *vp = p.v;
-      const int nv = chunk_ptrs(cn, kp, vp);
-      load_chunk(nxt, kp, vp, rs, nv, gam, r);
+  for (; ci < n_chunks; ci += 3 * kWaves) {
+#pragma unroll
+    for (int b = 0; b < 3; ++b) {
+      const int c = ci + b * kWaves;
+      if (b > 0 && c >= n_chunks) break;
+      const int tok0 = kv_begin + c * kChunk;
+      attend_chunk<NCB>(buf[b], qop, col_limit, tok0, tok0 + kChunk > mask_from, p.scale_log2, gam,
+                        m, lsum, acc);
+      chunk_rsrc(c + 3 * kWaves, rk, rv);
+      load_chunk(buf[b], rk, rv, k_off, v_off, urs);
     }
-    attend_chunk<NCB>(cur, qop, col_limit, kv_begin + ci * kChunk, kv_end, p.scale_log2, gam, m,
-                      lsum, acc);
-    cur = nxt;
   }
 
   // ---- merge the 4 waves ---------------------------------------------------
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) {
-    lsum[cb] += shfl_xor_f32(lsum[cb], 16);
+    lsum[cb] += shfl_xor_f32(lsum[cb], 16);   // once per partition
     lsum[cb] += shfl_xor_f32(lsum[cb], 32);
     if (gam == 0) {
       sm_ml[wave][16 * cb + r][0] = m[cb];
@@ -343,7 +355,7 @@ __global__ __launch_bounds__(256) void paged_mq_attn_kernel(MqParams p) {
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_ml[w][col][0]);
       const float Ms = (M == -INFINITY) ? 0.f : M;
-      const float sc = exp2f(m[cb] - Ms);
+      const float sc = fast_exp2(m[cb] - Ms);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         float* dst = &sm_o[wave][r][32 * gam + 8 * k];
@@ -367,7 +379,7 @@ __global__ __launch_bounds__(256) void paged_mq_attn_kernel(MqParams p) {
         const float Ms = (M == -INFINITY) ? 0.f : M;
         float L = 0.f;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) L += sm_ml[w][col][1] * exp2f(sm_ml[w][col][0] - Ms);
+        for (int w = 0; w < kWaves; ++w) L += sm_ml[w][col][1] * fast_exp2(sm_ml[w][col][0] - Ms);
         float o[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -430,14 +442,14 @@ __global__ __launch_bounds__(256) void mq_reduce_kernel(MqParams p) {
   for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, shfl_xor_f32(M, off));
   const float Ms = (M == -INFINITY) ? 0.f : M;
   float L = 0.f;
-  for (int q = lane; q < n_parts; q += 64) L += ml[2 * q + 1] * exp2f(ml[2 * q] - Ms);
+  for (int q = lane; q < n_parts; q += 64) L += ml[2 * q + 1] * fast_exp2(ml[2 * q] - Ms);
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) L += shfl_xor_f32(L, off);
 
   const float* pa = p.part_acc + rh * p.max_parts * kHeadDim + 2 * lane;
   float o0 = 0.f, o1 = 0.f;
   for (int q = 0; q < n_parts; ++q) {
-    const float w = exp2f(ml[2 * q] - Ms);
+    const float w = fast_exp2(ml[2 * q] - Ms);
     const f32x2 a = *reinterpret_cast<const f32x2*>(pa + (int64_t)q * kHeadDim);
     o0 += w * a.x;
     o1 += w * a.y;

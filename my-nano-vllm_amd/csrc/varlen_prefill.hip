@@ -227,23 +227,28 @@ __global__ __launch_bounds__(256) void varlen_prefill_kernel(PrefillParams p) {
       }
     }
     mx = fmaxf(mx, shfl_xor_f32(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = exp2f(m_run - m_use);
-    m_run = m_new;
+    // Lazy rescale (see kLazyRescaleLog2).
+    const bool grow = mx > m_run + kLazyRescaleLog2;
+    if (wave_any(grow)) {
+      const float m_new = grow ? mx : m_run;
+      const float alpha = grow ? fast_exp2(m_run - m_new) : 1.f;
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+    }
+    const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
     float ps = 0.f;
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const float e = exp2f(s[rb][i] - m_use);
+        const float e = fast_exp2(s[rb][i] - m_use);
         s[rb][i] = e;
         ps += e;
       }
     }
-    l_run = l_run * alpha + ps;
-#pragma unroll
-    for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+    l_run += ps;
 
     // ---- O^T += V^T . P^T ---------------------------------------------------------
 #pragma unroll
