@@ -89,7 +89,8 @@ int64_t nvamd_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t n
  * context_lens: int32 [batch].  A row with context 0 is written as zeros
  *   (the reference produces NaN there).
  * out = bf16(fp16(softmax(scale * q.K^T) . V)), fp32 accumulation.
- * part_tokens: split-KV partition length (multiple of 256) or 0 = automatic.
+ * part_tokens: split-KV partition length (multiple of 256, at most
+ *   63 blocks) or 0 = automatic.
  */
 int32_t nvamd_fp8_decode_attention(void* out, const void* q,
                                    const void* k_cache, const void* v_cache,
@@ -102,10 +103,12 @@ int32_t nvamd_fp8_decode_attention(void* out, const void* q,
 
 /* Workspace needed by nvamd_fp8_prefill_attention.  kv_cap is the static
  * upper bound of keys per sequence: max_num_blocks*block_size for the paged
- * layout, the number of K/V rows for the contiguous layout. */
+ * layout, the number of K/V rows for the contiguous layout.  block_size is
+ * the paged cache's block size, 0 for the contiguous layout. */
 int64_t nvamd_prefill_workspace_bytes(int64_t num_tokens, int32_t num_seqs, int32_t num_heads,
                                       int32_t num_kv_heads, int64_t kv_cap,
-                                      int32_t max_seqlen_q, int32_t part_tokens);
+                                      int32_t max_seqlen_q, int32_t block_size,
+                                      int32_t part_tokens);
 
 /*
  * Varlen causal prefill (chunked prefill over cached context and

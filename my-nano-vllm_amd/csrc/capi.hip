@@ -49,16 +49,33 @@ constexpr int kMqMaxCols = 32;        // query rows per kv head packed by the sp
 constexpr int kPartAlign = 256;       // partition lengths are multiples of 256 tokens
 constexpr int64_t kPartialFloats = kHeadDim + 2;  // acc[128] + (m, l) per partition
 
+// A paged partition spans at most this many KV blocks: the decode kernel
+// holds the partition's block-table entries in one wave-wide register
+// (64 lanes; one spare for a partition that starts inside a block).
+constexpr int64_t kMaxPartBlocks = 63;
+
+int64_t max_part_tokens(int32_t block_size) {
+  if (block_size <= 0) return INT64_MAX;  // contiguous layout: no table
+  return kMaxPartBlocks * block_size / kPartAlign * kPartAlign;
+}
+
+// kv heads per decode workgroup (the kernel reads HG*128-byte row slices).
+int64_t kv_head_groups(int32_t num_kv_heads) {
+  return (num_kv_heads % 2 == 0) ? num_kv_heads / 2 : num_kv_heads;
+}
+
 // Split-KV partition length from static shapes only (graph-safe): aim for
-// about 16 workgroups per CU when every sequence is at its capacity.
-int64_t choose_part_tokens(int64_t items, int64_t kv_cap, int64_t requested) {
+// about 4 workgroups per CU when every sequence is at its capacity, within
+// the block-table limit of a partition.
+int64_t choose_part_tokens(int64_t items, int64_t kv_cap, int64_t requested, int32_t block_size) {
   if (requested > 0) return requested;
+  const int64_t cap = max_part_tokens(block_size);
   items = std::max<int64_t>(items, 1);
-  const int64_t target = (int64_t)device_cu_count() * 16;
+  const int64_t target = (int64_t)device_cu_count() * 4;
   const int64_t parts = std::max<int64_t>((target + items - 1) / items, 1);
   int64_t part = (std::max<int64_t>(kv_cap, 1) + parts - 1) / parts;
   part = (part + kPartAlign - 1) / kPartAlign * kPartAlign;
-  return std::max<int64_t>(part, kPartAlign);
+  return std::min(std::max<int64_t>(part, kPartAlign), cap);
 }
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -94,7 +111,7 @@ int heads_per_workgroup(int g) {
 
 extern "C" {
 
-int32_t nvamd_abi_version(void) { return 1; }
+int32_t nvamd_abi_version(void) { return 2; }
 
 const char* nvamd_last_error(void) { return g_last_error.c_str(); }
 
@@ -123,7 +140,8 @@ int64_t nvamd_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t n
   if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || max_num_blocks <= 0 || block_size <= 0)
     return 0;
   const int64_t kv_cap = (int64_t)max_num_blocks * block_size;
-  const int64_t part = choose_part_tokens((int64_t)batch * num_kv_heads, kv_cap, part_tokens);
+  const int64_t part = choose_part_tokens((int64_t)batch * kv_head_groups(num_kv_heads), kv_cap,
+                                          part_tokens, block_size);
   return partial_bytes(batch, num_heads, ceil_div(kv_cap, part));
 }
 
@@ -141,6 +159,9 @@ int32_t nvamd_fp8_decode_attention(void* out, const void* q, const void* k_cache
     return fail(NVAMD_ERR_UNSUPPORTED, "%s: block_size must be a positive multiple of 64 (got %d)", fn, block_size);
   if (part_tokens < 0 || part_tokens % kPartAlign != 0)
     return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: part_tokens must be 0 or a multiple of %d", fn, kPartAlign);
+  if (part_tokens > max_part_tokens(block_size))
+    return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: part_tokens %d exceeds %lld (%lld blocks of %d)", fn,
+                part_tokens, (long long)max_part_tokens(block_size), (long long)kMaxPartBlocks, block_size);
   const int G = num_heads / num_kv_heads;
   if (G > kMqMaxCols)
     return fail(NVAMD_ERR_UNSUPPORTED, "%s: more than %d query heads per kv head", fn, kMqMaxCols);
@@ -167,7 +188,8 @@ int32_t nvamd_fp8_decode_attention(void* out, const void* q, const void* k_cache
   p.G = G;
   p.block_size = block_size;
   const int64_t kv_cap = (int64_t)max_num_blocks * block_size;
-  const int64_t part = choose_part_tokens((int64_t)batch * num_kv_heads, kv_cap, part_tokens);
+  const int64_t part = choose_part_tokens((int64_t)batch * kv_head_groups(num_kv_heads), kv_cap,
+                                          part_tokens, block_size);
   p.part_tokens = (int)part;
   p.max_parts = (int)ceil_div(kv_cap, part);
   p.mq_max_q = 1;
@@ -183,12 +205,13 @@ int32_t nvamd_fp8_decode_attention(void* out, const void* q, const void* k_cache
 
 int64_t nvamd_prefill_workspace_bytes(int64_t num_tokens, int32_t num_seqs, int32_t num_heads,
                                       int32_t num_kv_heads, int64_t kv_cap, int32_t max_seqlen_q,
-                                      int32_t part_tokens) {
+                                      int32_t block_size, int32_t part_tokens) {
   if (num_tokens <= 0 || num_seqs <= 0 || num_heads <= 0 || num_kv_heads <= 0 || kv_cap <= 0) return 0;
   const int G = num_heads / num_kv_heads;
   if (G <= 0 || G > kMqMaxCols) return 0;
   (void)max_seqlen_q;
-  const int64_t part = choose_part_tokens((int64_t)num_seqs * num_kv_heads, kv_cap, part_tokens);
+  const int64_t part = choose_part_tokens((int64_t)num_seqs * kv_head_groups(num_kv_heads), kv_cap,
+                                          part_tokens, block_size);
   return partial_bytes(num_tokens, num_heads, ceil_div(kv_cap, part));
 }
 
@@ -212,6 +235,9 @@ int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, con
     return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: block_tables has no columns", fn);
   if (part_tokens < 0 || part_tokens % kPartAlign != 0)
     return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: part_tokens must be 0 or a multiple of %d", fn, kPartAlign);
+  if (paged && part_tokens > max_part_tokens(block_size))
+    return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: part_tokens %d exceeds %lld (%lld blocks of %d)", fn,
+                part_tokens, (long long)max_part_tokens(block_size), (long long)kMaxPartBlocks, block_size);
   const int G = num_heads / num_kv_heads;
   if (G > kMqMaxCols)
     return fail(NVAMD_ERR_UNSUPPORTED, "%s: more than %d query heads per kv head", fn, kMqMaxCols);
@@ -241,7 +267,8 @@ int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, con
     p.Hkv = num_kv_heads;
     p.G = G;
     p.block_size = paged ? block_size : 64;
-    const int64_t part = choose_part_tokens((int64_t)num_seqs * num_kv_heads, kv_cap, part_tokens);
+    const int64_t part = choose_part_tokens((int64_t)num_seqs * kv_head_groups(num_kv_heads), kv_cap,
+                                            part_tokens, paged ? block_size : 0);
     p.part_tokens = (int)part;
     p.max_parts = (int)ceil_div(kv_cap, part);
     p.mq_max_q = std::min(mq_max_q, max_seqlen_q);

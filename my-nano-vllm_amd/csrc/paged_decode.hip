@@ -205,15 +205,102 @@ __device__ __forceinline__ void store_out_row8(uint16_t* __restrict__ dst, const
   *reinterpret_cast<u32x4*>(dst) = w;
 }
 
+// ---------------------------------------------------------------------------
+// LDS staging of the KV stream
+// ---------------------------------------------------------------------------
+// A workgroup owns HG kv heads (HG = 2 when Hkv is even, else 1), so every
+// token row it reads is a contiguous HG*128-byte slice of the cache row.  K
+// and V move HBM -> LDS with direct-to-LDS buffer loads (no VGPRs are held
+// while a load is in flight): one stage = kTS tokens of K then of V, 8 KiB
+// each, every load instruction fetching 1 KiB of whole 128-byte lines.  A
+// ring of kStages stages keeps two stages in flight while one is computed.
+//
+// The stage image in LDS is row-major [kTS rows][HG*128 bytes] with the
+// 16-byte granules of each row XOR-swizzled by (row & 7), so the operand
+// reads below (16 rows at one column, or 16 lanes along one row) hit
+// distinct banks.  The swizzle is applied on the fetch side: lane l of a load
+// instruction always lands at LDS offset 16*l and fetches the global granule
+// that belongs there.
+template <int HG>
+struct Stage {
+  static constexpr int kTS = 64 / HG;              // tokens per stage
+  static constexpr int kRowBytes = HG * kHeadDim;  // bytes of one token row in LDS
+  static constexpr int kHalf = kTS * kRowBytes;    // K (or V) bytes per stage: 8 KiB
+  static constexpr int kBytes = 2 * kHalf;         // 16 KiB
+  static constexpr int kRowsPerLoad = 8 / HG;      // token rows per 1 KiB load instruction
+  static constexpr int kLanesPerRow = 8 * HG;      // 16-byte granules per row
+  static constexpr int kWavesPerHead = kWaves / HG;
+};
+constexpr int kStages = 3;
+constexpr int kRingBytes = kStages * 16384;
+
+typedef __attribute__((address_space(3))) const uint8_t* lds_cptr_t;
+
+// LDS byte address (the M0 operand of a direct-to-LDS load) of a __shared__ pointer.
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
+  return (uint32_t)(uintptr_t)(lds_cptr_t)p;
+}
+
+// Raw buffer descriptor as four dwords (base, stride 0, num_records, word 3).
+__device__ __forceinline__ u32x4 rsrc_words(const void* base, uint32_t num_bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  return u32x4{(uint32_t)a, (uint32_t)(a >> 32) & 0xFFFFu, num_bytes, (uint32_t)kBufferRsrcWord3};
+}
+
+// Direct-to-LDS 16-byte load: lane l's 16 bytes at byte offset voff of the
+// buffer land at LDS address lds + 16*l; offsets at or past num_records
+// write zeros.  Issued as inline asm so that the compiler's wait-count
+// insertion does not treat the pending LDS write as a hazard on every later
+// LDS access (it would wait for all loads in flight); completion is tracked
+// explicitly with wait_vmcnt + lds_barrier.  s_nop: one wait state between
+// the M0 write and the LDS-DMA instruction that reads it.  The statement is
+// volatile, so it stays ordered with the barrier and s_waitcnt intrinsics;
+// no memory clobber is declared so the compiler can keep the block-table
+// reads on the scalar path (no kernel code stores to the cache or tables).
+// The M0 write needs no clobber: this code uses M0 only for these loads.
+__device__ __forceinline__ void dma_load16(u32x4 rsrc, uint32_t voff, uint32_t lds) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds"
+      :
+      : "s"(lds), "v"(voff), "s"(rsrc));
+}
+
+// Makes the compiler wait here for the loads that produced x (an empty asm
+// that reads it), so no load of x is still counted as pending inside the
+// main loop, where the compiler would otherwise wait for every load in flight.
+__device__ __forceinline__ void consume(const bf16x8& x) { asm volatile("" ::"v"(x)); }
+__device__ __forceinline__ void consume_i32(int x) { asm volatile("" ::"v"(x)); }
+
+__device__ __forceinline__ u32x4 lds_read16(const uint8_t* a) { return *reinterpret_cast<const u32x4*>(a); }
+__device__ __forceinline__ u32x2 lds_read8(const uint8_t* a) { return *reinterpret_cast<const u32x2*>(a); }
+
+// s_waitcnt vmcnt(n) (gfx9 encoding; expcnt and lgkmcnt left unconstrained).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier that orders LDS only: loads to VGPRs or LDS that are still
+// in flight stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 }  // namespace
 
-template <int NCB>
+template <int NCB, int HG>
 __global__ __launch_bounds__(256) void paged_mq_attn_kernel(MqParams p) {
-  __shared__ float sm_ml[kWaves][NCB * 16][2];
-  __shared__ __attribute__((aligned(16))) float sm_o[kWaves][16][kPitch];
+  using S = Stage<HG>;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kRingBytes];
+  const uint32_t lds_smem = wave_uniform((int)lds_addr(smem));
 
   const int part = blockIdx.x;
-  const int g = blockIdx.y;
+  const int hg = blockIdx.y;            // kv head group: heads hg*HG .. hg*HG+HG-1
   const int seq = blockIdx.z;
   const SeqGeom sg = seq_geom(p, seq);
   if (!sg.active) return;
@@ -221,18 +308,21 @@ __global__ __launch_bounds__(256) void paged_mq_attn_kernel(MqParams p) {
   const int lane = tid & 63, wave = wave_uniform(tid >> 6);
   const int gam = lane >> 4, r = lane & 15;
   const int G = p.G;
+  const int hh = wave / S::kWavesPerHead;        // head of this wave within the group
+  const int cw = wave % S::kWavesPerHead;        // its 16-token chunk within each stage
+  const int g = hg * HG + hh;                    // kv head of this wave
 
   const int kv_begin = part * p.part_tokens;
   if (sg.Lk <= 0) {
     // Empty context (graph padding rows): the reference yields NaN here; write 0.
     if (part == 0) {
-      for (int idx = tid; idx < sg.Lq * G * (kHeadDim / 8); idx += 256) {
+      for (int idx = tid; idx < sg.Lq * HG * G * (kHeadDim / 8); idx += 256) {
         const int col = idx / (kHeadDim / 8), d8 = idx % (kHeadDim / 8);
-        const int qi = col / G, gh = col - qi * G;
+        const int qi = col / (HG * G), gh = col - qi * (HG * G);
         const int64_t row = sg.row0 + qi;
         if (row >= p.q_rows) continue;
         u32x4 z = {0u, 0u, 0u, 0u};
-        *reinterpret_cast<u32x4*>(p.out + (row * p.Hq + g * G + gh) * kHeadDim + 8 * d8) = z;
+        *reinterpret_cast<u32x4*>(p.out + (row * p.Hq + hg * HG * G + gh) * kHeadDim + 8 * d8) = z;
       }
     }
     return;
@@ -275,120 +365,183 @@ __global__ __launch_bounds__(256) void paged_mq_attn_kernel(MqParams p) {
   }
 
   const int64_t rs = (int64_t)p.Hkv * kHeadDim;  // bytes between consecutive token rows
-  const int n_chunks = (kv_end - kv_begin + kChunk - 1) / kChunk;
-
-  // Buffer descriptors of chunk ci (wave-uniform), bounded to its valid rows.
-  // A chunk (32 tokens) never straddles a KV block (block_size % 64 == 0).
-  // Chunks past the partition get num_records = 0: their loads are still
-  // issued (so every loop path has the same number of loads in flight and
-  // the wait counts stay exact) but read nothing and return zeros.
-  auto chunk_rsrc = [&](int ci, __amdgpu_buffer_rsrc_t& rk, __amdgpu_buffer_rsrc_t& rv) {
-    const int t0 = kv_begin + ci * kChunk;
-    int nvalid = max(0, min(kChunk, kv_end - t0));
-    int64_t row = 0;
-    if (p.block_tables != nullptr) {
-      const int bi = min(t0 / p.block_size, (int)p.bt_stride - 1);
-      const int blk = wave_uniform(p.block_tables[(int64_t)seq * p.bt_stride + bi]);
-      row = (int64_t)blk * p.block_size + (t0 % p.block_size);
-      if (blk < 0 || row + kChunk > p.kv_rows) nvalid = 0;
-    } else {
-      row = (int64_t)sg.kv_row0 + t0;
-      if (row < 0 || row + nvalid > p.kv_rows) nvalid = 0;
-    }
-    if (nvalid == 0) row = 0;
-    const int64_t base = (row * p.Hkv + g) * kHeadDim;
-    rk = make_rsrc(p.k + base, (uint32_t)(nvalid * rs));
-    rv = make_rsrc(p.v + base, (uint32_t)(nvalid * rs));
-  };
-
-  const uint32_t urs = (uint32_t)rs;
-  const uint32_t k_off = (uint32_t)r * urs + 16u * gam;
-  const uint32_t v_off = 4u * gam * urs + 8u * r;
+  const int n_st = (kv_end - kv_begin + S::kTS - 1) / S::kTS;  // stages of this partition
   // Masking is needed only on chunks that reach past the smallest visible
   // limit of any column (or past the partition end, whose rows read as 0).
   const int mask_from = min(kv_end, sg.Lk - sg.Lq + 1);
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) col_limit[cb] = min(col_limit[cb], kv_end);
 
-  // Three register buffers in rotation, all always in flight: while one
-  // chunk is computed the next two are loading.  Every path into the loop
-  // head has the same loads outstanding, so each compute waits only for its
-  // own buffer.
-  ChunkRegs buf[3];
-  __amdgpu_buffer_rsrc_t rk, rv;
-  int ci = wave;
+  // ---- fetch side: this wave's two K and two V load instructions per stage --
+  // Instruction j (= 2*wave + i) covers stage rows [j*kRowsPerLoad, +kRowsPerLoad);
+  // lane l fetches row j*kRowsPerLoad + l/kLanesPerRow, granule
+  // (l % kLanesPerRow) ^ (row & 7), and lands at LDS offset j*1024 + 16*l.
+  uint32_t fetch_off[2];
 #pragma unroll
-  for (int b = 0; b < 3; ++b) {
-    chunk_rsrc(ci + b * kWaves, rk, rv);
-    load_chunk(buf[b], rk, rv, k_off, v_off, urs);
+  for (int i = 0; i < 2; ++i) {
+    const int row = (2 * wave + i) * S::kRowsPerLoad + lane / S::kLanesPerRow;
+    const int gran = (lane % S::kLanesPerRow) ^ (row & 7);
+    fetch_off[i] = (uint32_t)row * (uint32_t)rs + 16u * (uint32_t)gran;
   }
-  for (; ci < n_chunks; ci += 3 * kWaves) {
+
+  // Stage cursor (paged layout): a stage never straddles a KV block
+  // (block_size % 64 == 0).  The partition's block-table entries are loaded
+  // once, lane l holding entry first_bi + l (a partition spans at most
+  // kMaxPartBlocks blocks, enforced by the host), and read in the loop with
+  // v_readlane, so the loop issues no memory reads besides the stages.
+  // Table indices are clamped into the row: entries past the partition are
+  // never dereferenced (their stages get zero-length descriptors).
+  const bool paged = p.block_tables != nullptr;
+  int ld_tok = kv_begin;
+  int ld_bi = 0, ld_off = 0, bt_lane = 0;
+  if (paged) {
+    const int first_bi = kv_begin / p.block_size;
+    ld_off = kv_begin - first_bi * p.block_size;
+    const int bi = min(first_bi + lane, (int)p.bt_stride - 1);
+    bt_lane = p.block_tables[(int64_t)seq * p.bt_stride + bi];
+  }
+  auto cur_block = [&]() -> int { return __builtin_amdgcn_readlane(bt_lane, min(ld_bi, 63)); };
+
+  // Issues this wave's share of the cursor's stage into ring slot `slot`
+  // and advances the cursor.  Rows past the partition (or an invalid block)
+  // get a zero-length descriptor: the loads are still issued, so every
+  // iteration has the same loads in flight, but they read nothing and write
+  // zeros.
+  auto issue_stage = [&](int slot) {
+    int nvalid = max(0, min(S::kTS, kv_end - ld_tok));
+    int64_t row;
+    if (paged) {
+      const int blk = cur_block();
+      row = (int64_t)blk * p.block_size + ld_off;
+      if (blk < 0 || row + S::kTS > p.kv_rows) nvalid = 0;
+    } else {
+      row = (int64_t)sg.kv_row0 + ld_tok;
+      if (row < 0 || row + nvalid > p.kv_rows) nvalid = 0;
+    }
+    if (nvalid == 0) row = 0;
+    const int64_t base = (row * p.Hkv + hg * HG) * kHeadDim;
+    const uint32_t nbytes = (uint32_t)(nvalid * rs);
+    const u32x4 rk = rsrc_words(p.k + base, nbytes);
+    const u32x4 rv = rsrc_words(p.v + base, nbytes);
+    const uint32_t dst = lds_smem + (uint32_t)(slot * S::kBytes + (2 * wave) * 1024);
+    dma_load16(rk, fetch_off[0], dst);
+    dma_load16(rk, fetch_off[1], dst + 1024u);
+    dma_load16(rv, fetch_off[0], dst + (uint32_t)S::kHalf);
+    dma_load16(rv, fetch_off[1], dst + (uint32_t)S::kHalf + 1024u);
+    ld_tok += S::kTS;
+    ld_off += S::kTS;
+    if (ld_off >= p.block_size) {
+      ld_off -= p.block_size;
+      ++ld_bi;
+    }
+  };
+
+  // ---- read side: this wave's operands of one stage --------------------------
+  // K: row 16cw + r, logical granules 8hh + gam and 8hh + 4 + gam.
+  // V: rows 16cw + 4gam + e, bytes [8r, +8) of head hh.
+  uint32_t k_rd[2], v_rd[4];
+  {
+    const int row = 16 * cw + r;
 #pragma unroll
-    for (int b = 0; b < 3; ++b) {
-      const int c = ci + b * kWaves;
-      if (b > 0 && c >= n_chunks) break;
-      const int tok0 = kv_begin + c * kChunk;
-      attend_chunk<NCB>(buf[b], qop, col_limit, tok0, tok0 + kChunk > mask_from, p.scale_log2, gam,
-                        m, lsum, acc);
-      chunk_rsrc(c + 3 * kWaves, rk, rv);
-      load_chunk(buf[b], rk, rv, k_off, v_off, urs);
+    for (int i = 0; i < 2; ++i)
+      k_rd[i] = (uint32_t)(row * S::kRowBytes + 16 * ((8 * hh + 4 * i + gam) ^ (row & 7)));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int rv = 16 * cw + 4 * gam + e;
+      v_rd[e] = (uint32_t)(S::kHalf + rv * S::kRowBytes + 16 * ((8 * hh + (r >> 1)) ^ (rv & 7)) + 8 * (r & 1));
     }
   }
 
-  // ---- merge the 4 waves ---------------------------------------------------
+  // ---- main loop: one stage per iteration, two more in flight --------------
+  issue_stage(0);
+  issue_stage(1);
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) consume(qop[cb][c]);
+  consume_i32(bt_lane);
+  int tok0 = kv_begin + 16 * cw;
+  for (int s = 0; s < n_st; ++s) {
+    wait_vmcnt<4>();   // this wave's loads of stage s have landed (stage s+1's 4 may not)
+    lds_barrier();     // ... and every wave's; slot (s+2)%3 is no longer being read
+    issue_stage((s + 2) % kStages);
+    const uint8_t* sl = smem + (s % kStages) * S::kBytes;
+    ChunkRegs cr;
+    cr.k[0] = lds_read16(sl + k_rd[0]);
+    cr.k[1] = lds_read16(sl + k_rd[1]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) cr.v[e] = lds_read8(sl + v_rd[e]);
+    attend_chunk<NCB>(cr, qop, col_limit, tok0, tok0 + kChunk > mask_from, p.scale_log2, gam, m, lsum,
+                      acc);
+    tok0 += S::kTS;
+  }
+
+  // ---- merge the waves of each head ------------------------------------------
+  wait_vmcnt<0>();     // the ring is reused below: no load may still be landing
+  lds_barrier();
+  float* sm_o = reinterpret_cast<float*>(smem);                      // [4 waves][16][kPitch]
+  float* sm_ml = sm_o + kWaves * 16 * kPitch;                         // [4 waves][NCB*16][2]
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) {
     lsum[cb] += shfl_xor_f32(lsum[cb], 16);   // once per partition
     lsum[cb] += shfl_xor_f32(lsum[cb], 32);
     if (gam == 0) {
-      sm_ml[wave][16 * cb + r][0] = m[cb];
-      sm_ml[wave][16 * cb + r][1] = lsum[cb];
+      sm_ml[(wave * NCB * 16 + 16 * cb + r) * 2 + 0] = m[cb];
+      sm_ml[(wave * NCB * 16 + 16 * cb + r) * 2 + 1] = lsum[cb];
     }
   }
-  __syncthreads();
+  lds_barrier();
 
+  const int c16 = (tid >> 4) & 15;   // output column within the block
+  const int d0 = 8 * (tid & 15);     // 8 output dims
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) {
     {
       const int col = 16 * cb + r;
       float M = -INFINITY;
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_ml[w][col][0]);
+      for (int k = 0; k < S::kWavesPerHead; ++k)
+        M = fmaxf(M, sm_ml[((hh * S::kWavesPerHead + k) * NCB * 16 + col) * 2]);
       const float Ms = (M == -INFINITY) ? 0.f : M;
       const float sc = fast_exp2(m[cb] - Ms);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        float* dst = &sm_o[wave][r][32 * gam + 8 * k];
+        float* dst = sm_o + (wave * 16 + r) * kPitch + 32 * gam + 8 * k;
         f32x4 lo = {acc[cb][0][k] * sc, acc[cb][1][k] * sc, acc[cb][2][k] * sc, acc[cb][3][k] * sc};
         f32x4 hi = {acc[cb][4][k] * sc, acc[cb][5][k] * sc, acc[cb][6][k] * sc, acc[cb][7][k] * sc};
         *reinterpret_cast<f32x4*>(dst) = lo;
         *reinterpret_cast<f32x4*>(dst + 4) = hi;
       }
     }
-    __syncthreads();
-    {
-      const int c16 = tid >> 4;          // column within the block
-      const int d0 = 8 * (tid & 15);     // 8 output dims
+    lds_barrier();
+    // 256 threads: 16 columns x 16 dim-octets, repeated for each head of the group.
+#pragma unroll
+    for (int oh = 0; oh < HG; ++oh) {
       const int col = 16 * cb + c16;
       const int qi = col / G, gh = col - qi * G;
       const int64_t row = sg.row0 + qi;
       if (qi < sg.Lq && row < p.q_rows) {
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_ml[w][col][0]);
+        for (int k = 0; k < S::kWavesPerHead; ++k)
+          M = fmaxf(M, sm_ml[((oh * S::kWavesPerHead + k) * NCB * 16 + col) * 2]);
         const float Ms = (M == -INFINITY) ? 0.f : M;
         float L = 0.f;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) L += sm_ml[w][col][1] * fast_exp2(sm_ml[w][col][0] - Ms);
+        for (int k = 0; k < S::kWavesPerHead; ++k) {
+          const float* e = sm_ml + ((oh * S::kWavesPerHead + k) * NCB * 16 + col) * 2;
+          L += e[1] * fast_exp2(e[0] - Ms);
+        }
         float o[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           float t = 0.f;
 #pragma unroll
-          for (int w = 0; w < kWaves; ++w) t += sm_o[w][c16][d0 + e];
+          for (int k = 0; k < S::kWavesPerHead; ++k)
+            t += sm_o[((oh * S::kWavesPerHead + k) * 16 + c16) * kPitch + d0 + e];
           o[e] = t;
         }
-        const int64_t rh = row * p.Hq + g * G + gh;
+        const int64_t rh = row * p.Hq + (hg * HG + oh) * G + gh;
         if (n_parts == 1) {
           const float inv = (L > 0.f) ? 1.0f / L : 0.f;
           store_out_row8(p.out + rh * kHeadDim + d0, o, inv);
@@ -404,7 +557,7 @@ __global__ __launch_bounds__(256) void paged_mq_attn_kernel(MqParams p) {
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
   }
 }
 
@@ -461,10 +614,14 @@ __global__ __launch_bounds__(256) void mq_reduce_kernel(MqParams p) {
 
 hipError_t launch_paged_mq(const MqParams& p, int ncb, hipStream_t stream) {
   if (p.num_seqs == 0) return hipSuccess;
-  const dim3 grid((unsigned)p.max_parts, (unsigned)p.Hkv, (unsigned)p.num_seqs);
-  switch (ncb) {
-    case 1: hipLaunchKernelGGL(paged_mq_attn_kernel<1>, grid, dim3(256), 0, stream, p); break;
-    case 2: hipLaunchKernelGGL(paged_mq_attn_kernel<2>, grid, dim3(256), 0, stream, p); break;
+  const int hg = (p.Hkv % 2 == 0) ? 2 : 1;  // kv heads per workgroup
+  const dim3 grid((unsigned)p.max_parts, (unsigned)(p.Hkv / hg), (unsigned)p.num_seqs);
+  const int variant = 2 * (ncb - 1) + (hg - 1);
+  switch (variant) {
+    case 0: hipLaunchKernelGGL((paged_mq_attn_kernel<1, 1>), grid, dim3(256), 0, stream, p); break;
+    case 1: hipLaunchKernelGGL((paged_mq_attn_kernel<1, 2>), grid, dim3(256), 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((paged_mq_attn_kernel<2, 1>), grid, dim3(256), 0, stream, p); break;
+    case 3: hipLaunchKernelGGL((paged_mq_attn_kernel<2, 2>), grid, dim3(256), 0, stream, p); break;
     default: return hipErrorInvalidValue;
   }
   hipError_t e = hipGetLastError();

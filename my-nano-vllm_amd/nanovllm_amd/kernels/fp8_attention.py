@@ -157,7 +157,7 @@ def fp8_prefill_attention(
         return out
     max_seqlen_q = int(max_seqlen_q)
     ws_bytes = lib.nvamd_prefill_workspace_bytes(num_tokens, num_seqs, num_heads, num_kv_heads,
-                                                 kv_cap, max_seqlen_q, 0)
+                                                 kv_cap, max_seqlen_q, block_size, 0)
     ws, ws_bytes = _workspace(ws_bytes, q.device)
     status = lib.nvamd_fp8_prefill_attention(
         out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), bt_ptr,
