@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <string>
@@ -45,6 +46,8 @@ int device_cu_count() {
 }
 
 constexpr int kHeadDim = 128;
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 constexpr int kMqMaxCols = 32;        // query rows per kv head packed by the split-KV kernel
 constexpr int kPartAlign = 256;       // partition lengths are multiples of 256 tokens
 constexpr int64_t kPartialFloats = kHeadDim + 2;  // acc[128] + (m, l) per partition
@@ -78,8 +81,6 @@ int64_t choose_part_tokens(int64_t items, int64_t kv_cap, int64_t requested, int
   return std::min(std::max<int64_t>(part, kPartAlign), cap);
 }
 
-int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
-
 int64_t partial_bytes(int64_t rows, int64_t heads, int64_t max_parts) {
   if (max_parts <= 1) return 0;
   return rows * heads * max_parts * kPartialFloats * (int64_t)sizeof(float);
@@ -105,6 +106,19 @@ int heads_per_workgroup(int g) {
   if (g % 4 == 0) return 4;
   if (g % 2 == 0) return 2;
   return 1;
+}
+
+int64_t align_up(int64_t n) { return (n + 255) / 256 * 256; }
+
+// Prefill kernel geometry for G query heads per kv head.
+int prefill_bm(int g) { return 128 / heads_per_workgroup(g); }
+
+// Bytes of the prefill work list (0 when every sequence takes the
+// short-query path).
+int64_t schedule_bytes(int32_t num_seqs, int g, int32_t max_seqlen_q) {
+  const int mq_max_q = kMqMaxCols / g;
+  if (max_seqlen_q <= mq_max_q) return 0;
+  return (int64_t)num_seqs * ceil_div(max_seqlen_q, prefill_bm(g)) * 8;
 }
 
 }  // namespace
@@ -153,6 +167,8 @@ int32_t nvamd_fp8_decode_attention(void* out, const void* q, const void* k_cache
                                    void* workspace, int64_t workspace_bytes, void* stream) {
   static const char* fn = "fp8_decode_attention";
   if (int32_t e = check_heads(fn, num_heads, num_kv_heads, head_dim)) return e;
+  if (!(softmax_scale > 0.f) || !std::isfinite(softmax_scale))
+    return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: softmax_scale must be positive and finite", fn);
   if (batch < 0 || num_blocks < 0 || max_num_blocks < 0)
     return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: negative size", fn);
   if (block_size <= 0 || block_size % 64 != 0)
@@ -209,10 +225,10 @@ int64_t nvamd_prefill_workspace_bytes(int64_t num_tokens, int32_t num_seqs, int3
   if (num_tokens <= 0 || num_seqs <= 0 || num_heads <= 0 || num_kv_heads <= 0 || kv_cap <= 0) return 0;
   const int G = num_heads / num_kv_heads;
   if (G <= 0 || G > kMqMaxCols) return 0;
-  (void)max_seqlen_q;
   const int64_t part = choose_part_tokens((int64_t)num_seqs * kv_head_groups(num_kv_heads), kv_cap,
                                           part_tokens, block_size);
-  return partial_bytes(num_tokens, num_heads, ceil_div(kv_cap, part));
+  const int64_t partials = partial_bytes(num_tokens, num_heads, ceil_div(kv_cap, part));
+  return align_up(partials) + schedule_bytes(num_seqs, G, max_seqlen_q);
 }
 
 int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, const void* v,
@@ -226,6 +242,8 @@ int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, con
   static const char* fn = "fp8_prefill_attention";
   (void)max_seqlen_k;
   if (int32_t e = check_heads(fn, num_heads, num_kv_heads, head_dim)) return e;
+  if (!(softmax_scale > 0.f) || !std::isfinite(softmax_scale))
+    return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: softmax_scale must be positive and finite", fn);
   if (num_tokens < 0 || num_seqs < 0 || num_kv_rows < 0 || max_seqlen_q < 0)
     return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: negative size", fn);
   const bool paged = block_tables != nullptr;
@@ -247,6 +265,14 @@ int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, con
 
   const int mq_max_q = kMqMaxCols / G;
   const int64_t kv_cap = paged ? (int64_t)max_num_blocks * block_size : std::max<int64_t>(num_kv_rows, 1);
+  const int64_t part = choose_part_tokens((int64_t)num_seqs * kv_head_groups(num_kv_heads), kv_cap,
+                                          part_tokens, paged ? block_size : 0);
+  const int64_t partials = partial_bytes(num_tokens, num_heads, ceil_div(kv_cap, part));
+  const int64_t sched = schedule_bytes(num_seqs, G, max_seqlen_q);
+  const int64_t need = align_up(partials) + sched;
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail(NVAMD_ERR_WORKSPACE, "%s: workspace of %lld bytes required (got %lld)", fn,
+                (long long)need, (long long)workspace_bytes);
 
   // Short-query sequences: split-KV multi-query kernel.
   {
@@ -267,17 +293,11 @@ int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, con
     p.Hkv = num_kv_heads;
     p.G = G;
     p.block_size = paged ? block_size : 64;
-    const int64_t part = choose_part_tokens((int64_t)num_seqs * kv_head_groups(num_kv_heads), kv_cap,
-                                            part_tokens, paged ? block_size : 0);
     p.part_tokens = (int)part;
     p.max_parts = (int)ceil_div(kv_cap, part);
     p.mq_max_q = std::min(mq_max_q, max_seqlen_q);
     p.scale_log2 = softmax_scale * 1.4426950408889634f;
-    const int64_t need = partial_bytes(p.q_rows, p.Hq, p.max_parts);
-    if (need > 0 && (workspace == nullptr || workspace_bytes < need))
-      return fail(NVAMD_ERR_WORKSPACE, "%s: workspace of %lld bytes required (got %lld)", fn,
-                  (long long)need, (long long)workspace_bytes);
-    set_partials(p, need > 0 ? workspace : nullptr);
+    set_partials(p, partials > 0 ? workspace : nullptr);
     const int ncb = (G * p.mq_max_q + 15) / 16;
     hipError_t e = nvamd::launch_paged_mq(p, ncb, (hipStream_t)stream);
     if (e != hipSuccess) return launch_status(e, fn);
@@ -307,7 +327,8 @@ int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, con
     p.block_size = paged ? block_size : 64;
     p.mq_max_q = mq_max_q;
     p.scale_log2 = softmax_scale * 1.4426950408889634f;
-    hipError_t e = nvamd::launch_varlen_prefill(p, (hipStream_t)stream);
+    void* schedule = static_cast<char*>(workspace) + align_up(partials);
+    hipError_t e = nvamd::launch_varlen_prefill(p, schedule, (hipStream_t)stream);
     if (e != hipSuccess) return launch_status(e, fn);
   }
   return ok();

@@ -59,6 +59,11 @@ hipError_t launch_kv_store(const void* key, int64_t key_stride, const void* valu
 
 hipError_t launch_paged_mq(const MqParams& p, int ncb, hipStream_t stream);
 
-hipError_t launch_varlen_prefill(const PrefillParams& p, hipStream_t stream);
+// Device bytes of the work list the prefill launch writes (sorted items).
+int64_t prefill_schedule_bytes(const PrefillParams& p);
+
+// Launches the schedule pass and the prefill kernel; `schedule` points to
+// prefill_schedule_bytes(p) bytes of device scratch.
+hipError_t launch_varlen_prefill(const PrefillParams& p, void* schedule, hipStream_t stream);
 
 }  // namespace nvamd
