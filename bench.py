@@ -1,20 +1,39 @@
 """Benchmark of the MI355X FP8 paged-attention hot path (one GPU).
 
-Headline: FP8 paged decode at Qwen3-0.6B attention shapes (16 query / 8 kv
-heads, head_dim 128, block 256, B = 256 sequences, context U[100, 2048]),
-reported as achieved HBM GB/s over the algorithmic bytes (each FP8 K/V byte
-once + bf16 Q/O + block-table row + context length).  Secondary fields:
-varlen chunked prefill at Qwen3-8B shapes (16 x 512-token chunks over
-cached context U[0, 4096]) in TFLOP/s of unmasked causal pairs, and the
-long-context split-KV decode at Qwen3-32B shapes.
+Headline (``value``): FP8 paged decode at Qwen3-0.6B attention shapes (16
+query / 8 kv heads, head_dim 128, block 256, B = 256 sequences, context
+U[100, 2048], seeded), as achieved HBM GB/s over the algorithmic bytes of a
+step: each FP8 K/V byte once + bf16 Q in and O out + the block-table row and
+context length of every sequence.  At this shape one decode call is one
+kernel launch (``paged_mq_attn_kernel``; the split-KV reduce is not needed),
+so the HIP-event time of a call is that kernel's duration.
+
+Secondary fields in the same JSON line:
+  prefill      varlen chunked prefill at Qwen3-8B shapes (32/8 heads, 16 x
+               512-token chunks over cached context U[0, 4096]) in TFLOP/s of
+               unmasked causal pairs, vs the bf16 dense MFMA peak;
+  long_decode  split-KV decode at Qwen3-32B shapes (64/8 heads, B = 32,
+               context U[32K, 128K], 1% of K/V x20).
 
 Inputs are resident in HBM before timing; two KV pools with different
 contents are alternated so the working set stays far above the 256 MB
-last-level cache.  Each timed region is bracketed by synchronisation and
-measured with HIP events on the stream the kernels are launched on.
+last-level cache.  The timed region is bracketed by synchronisation and
+measured with HIP events recorded on the stream the kernels are launched on
+(torch's current stream).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only decode|prefill|long|all]
-                    [--no-cpu-baseline]
+``roofline.traffic`` comes from the committed rocprofv3 counter summary
+(profiles/decode_qwen3_0p6b_b256_pmc.json: FETCH_SIZE / WRITE_SIZE of the
+decode kernel, each scaled by the same counter's reading for a plain copy
+of known size, which ``--copy-probe`` runs); it is null if that file is
+absent.
+
+``cpu_baseline`` times the oracle (torch-CPU dequant + fp32 attention, the
+parity tests' checker) on the host cores for a bounded sample of the same
+workload.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                    [--only decode|prefill|long|all] [--no-cpu-baseline]
+                    [--copy-probe]
 """
 import argparse
 import json
@@ -35,6 +54,9 @@ from nanovllm_amd.layers.attention import store_kvcache  # noqa: E402
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 SCALE = 128 ** -0.5
+METRIC = "decode attn HBM GB/s (%peak) + prefill attn TFLOP/s, Qwen3-8B shapes, FP8 KV"
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "decode_qwen3_0p6b_b256_pmc.json")
+COPY_PROBE_BYTES = 1 << 30
 
 
 def parse():
@@ -44,6 +66,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", default="all", choices=["decode", "prefill", "long", "all"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run a plain 1 GiB device copy (counter scale for rocprofv3 --pmc)")
     return ap.parse_args()
 
 
@@ -52,17 +76,19 @@ def log(msg):
 
 
 def timed(fn, steps, warmup):
-    """Median-free average: HIP events around `steps` back-to-back calls."""
-    for _ in range(warmup):
-        fn(0)
+    """Average ms per call over `steps` back-to-back calls, HIP events on the
+    current stream (the stream the kernels are launched on)."""
+    for i in range(warmup):
+        fn(i)
+    stream = torch.cuda.current_stream()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
+    start.record(stream)
     for i in range(steps):
         fn(i)
-    end.record()
+    end.record(stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps  # ms
+    return start.elapsed_time(end) / steps
 
 
 def gpu_pools(wl, n_pools):
@@ -109,29 +135,41 @@ def bench_prefill(wl, steps, warmup, n_pools=2):
     return dict(ms=ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12), pools, q
 
 
-def cpu_baseline_decode(wl, pool, q, n_seqs=64, repeats=3):
+def copy_probe(reps=4):
+    """A plain device copy of known size: its FETCH_SIZE / WRITE_SIZE readings
+    under rocprofv3 --pmc give the counters' scale."""
+    src = torch.full((COPY_PROBE_BYTES,), 7, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copy probe: {reps} x {COPY_PROBE_BYTES} bytes")
+
+
+def cpu_baseline_decode(wl, pool, q, target_s=12.0):
     """The oracle (torch-CPU dequant + fp32 attention) on a bounded sample of
-    the same workload: the first `n_seqs` sequences, same cache bytes."""
+    the same workload: whole passes over all sequences, same cache bytes,
+    repeated until about `target_s` seconds of CPU work."""
     from oracle import attention as oa
-    sub = W.sub_workload(wl, range(min(n_seqs, wl.num_seqs)))
     kc = pool[0].view(torch.uint8).cpu()
     vc = pool[1].view(torch.uint8).cpu()
-    qc = q[:sub.num_seqs].cpu()
-    bt = torch.from_numpy(sub.block_tables)
-    ctx = torch.from_numpy(sub.context_lens())
+    qc = q[:wl.num_seqs].cpu()
+    bt = torch.from_numpy(wl.block_tables)
+    ctx = torch.from_numpy(wl.context_lens())
     torch.set_num_threads(os.cpu_count() or 1)
     oa.decode_attention(qc, kc, vc, bt, ctx, SCALE)  # warm-up
     times = []
-    for _ in range(repeats):
+    t_start = time.perf_counter()
+    while time.perf_counter() - t_start < target_s or len(times) < 3:
         t0 = time.perf_counter()
         oa.decode_attention(qc, kc, vc, bt, ctx, SCALE)
         times.append(time.perf_counter() - t0)
     t = statistics.median(times)
-    return dict(value=round(sub.decode_bytes() / t / 1e9, 4), unit="GB/s",
+    return dict(value=round(wl.decode_bytes() / t / 1e9, 4), unit="GB/s",
                 cores=torch.get_num_threads(), kind="port",
-                sample=f"first {sub.num_seqs} of {wl.num_seqs} sequences of {wl.name} "
-                       f"({sub.decode_bytes() / 1e6:.1f} MB algorithmic), median of {repeats} "
-                       f"runs of {t:.3f}s; cpu={_cpu_model()}")
+                sample=f"all {wl.num_seqs} sequences of {wl.name} ({wl.decode_bytes() / 1e6:.1f} MB "
+                       f"algorithmic) per pass, median of {len(times)} passes of {t:.3f}s "
+                       f"({sum(times):.1f}s total); cpu={_cpu_model()}")
 
 
 def _cpu_model():
@@ -145,11 +183,21 @@ def _cpu_model():
     return "unknown"
 
 
+def _traffic_from_profile():
+    """HBM bytes per decode launch from the committed counter summary."""
+    try:
+        with open(PMC_SUMMARY) as f:
+            d = json.load(f)
+        return int(d["hbm_bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no "
-              "multi-GPU path -- run with --gpus 1", file=sys.stderr)
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build has no "
+              "multi-GPU path; run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
@@ -157,23 +205,25 @@ def main():
     torch.cuda.set_device(0)
     line = {}
     extra = {}
+    if args.copy_probe:
+        copy_probe()
 
     if args.only in ("decode", "all"):
         wl = W.qwen3_0p6b_decode()
         log(f"decode workload {wl.name}: B={wl.num_seqs} bytes={wl.decode_bytes()}")
         res, pools, q = bench_decode(wl, args.steps, args.warmup)
         log(f"decode: {res['ms'] * 1e3:.1f} us/step, {res['gbs']:.1f} GB/s")
-        line.update(metric="decode attn HBM GB/s (%peak) + prefill attn TFLOP/s, Qwen3-8B shapes, FP8 KV",
-                    value=round(res["gbs"], 2), unit="GB/s", ms_per_step=round(res["ms"], 5),
+        line.update(metric=METRIC, value=round(res["gbs"], 2), unit="GB/s",
+                    ms_per_step=round(res["ms"], 5),
                     roofline=dict(bound="hbm", achieved=round(res["gbs"], 2), peak=HBM_PEAK_GBS,
                                   unit="GB/s", frac=round(res["gbs"] / HBM_PEAK_GBS, 4),
-                                  traffic=None, kernel="paged_mq_attn_kernel<1> + mq_reduce_kernel",
-                                  algorithmic_bytes_per_step=res["bytes"]),
+                                  traffic=_traffic_from_profile(), kernel="paged_mq_attn_kernel<1,2>",
+                                  algorithmic_bytes_per_launch=res["bytes"]),
                     config=dict(workload=wl.name, batch=wl.num_seqs, num_heads=wl.num_heads,
                                 num_kv_heads=wl.num_kv_heads, head_dim=128, block_size=wl.block_size,
                                 context="uniform[100,2048]", kv_dtype="float8_e4m3fn", kv_pools=2))
         if not args.no_cpu_baseline:
-            log("cpu baseline (oracle) on a sample of the decode workload")
+            log("cpu baseline (oracle) on the decode workload")
             line["cpu_baseline"] = cpu_baseline_decode(wl, pools[0], q)
         del pools
         torch.cuda.empty_cache()
@@ -186,7 +236,8 @@ def main():
         extra["prefill"] = dict(workload=wl.name, ms_per_step=round(res["ms"], 5),
                                 tflops=round(res["tflops"], 2),
                                 frac_bf16_peak=round(res["tflops"] / BF16_PEAK_TFLOPS, 4),
-                                algorithmic_flops_per_step=res["flops"], kernel="varlen_prefill_kernel")
+                                algorithmic_flops_per_step=res["flops"],
+                                kernels="prefill_schedule_kernel + varlen_prefill_kernel + paged_mq_attn_kernel")
         del pools
         torch.cuda.empty_cache()
 
@@ -197,18 +248,20 @@ def main():
         log(f"long decode: {res['ms'] * 1e3:.1f} us/step, {res['gbs']:.1f} GB/s")
         extra["long_decode"] = dict(workload=wl.name, ms_per_step=round(res["ms"], 5),
                                     gbs=round(res["gbs"], 2), frac_hbm_peak=round(res["gbs"] / HBM_PEAK_GBS, 4),
-                                    algorithmic_bytes_per_step=res["bytes"])
+                                    algorithmic_bytes_per_step=res["bytes"],
+                                    kernels="paged_mq_attn_kernel<1,2> + mq_reduce_kernel")
         del pools
         torch.cuda.empty_cache()
 
     if "value" not in line:   # partial runs (profiling) still print one line
         first = next(iter(extra.values()))
-        line.update(metric="partial run", value=first.get("tflops", first.get("gbs")),
+        line.update(metric=METRIC + " (partial run: " + first["workload"] + ")",
+                    value=first.get("tflops", first.get("gbs")),
                     unit="TFLOP/s" if "tflops" in first else "GB/s", ms_per_step=first["ms_per_step"],
                     config=dict(workload=first["workload"]))
     line.update(n_gpus=1, steps=args.steps, warmup=args.warmup, higher_is_better=True, scaling="weak",
-                vs_baseline=None, dtype="fp8_e4m3 kv -> bf16 mfma, fp32 accumulate, bf16 out",
-                data="synthetic (seeded N(0,1) bf16 quantised to E4M3)")
+                vs_baseline=None, dtype="bf16",
+                data="synthetic (seeded N(0,1) bf16, K/V quantised to FP8 E4M3 by the store kernel)")
     line.update(extra)
     print(json.dumps(line), flush=True)
 

@@ -561,28 +561,8 @@ __global__ __launch_bounds__(256) void paged_mq_attn_kernel(MqParams p) {
   }
 }
 
-// One wave per (query row, head): log-sum-exp merge of the partitions.
-__global__ __launch_bounds__(256) void mq_reduce_kernel(MqParams p) {
-  const int lane = threadIdx.x & 63;
-  const int64_t rh = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (rh >= p.q_rows * p.Hq) return;
-  const int64_t row = rh / p.Hq;
-  int Lk;
-  if (p.cu_q != nullptr) {
-    // sequence owning this row: largest s with cu_q[s] <= row
-    int lo = 0, hi = p.num_seqs;  // invariant: cu_q[lo] <= row < cu_q[hi]
-    if (row >= p.cu_q[p.num_seqs] || row < p.cu_q[0]) return;
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (p.cu_q[mid] <= row) lo = mid; else hi = mid;
-    }
-    const int Lq = p.cu_q[lo + 1] - p.cu_q[lo];
-    if (Lq <= 0 || Lq > p.mq_max_q) return;
-    Lk = p.cu_k[lo + 1] - p.cu_k[lo];
-  } else {
-    if (row >= p.num_seqs) return;
-    Lk = p.context_lens[row];
-  }
+// Log-sum-exp merge of the partitions of one (query row, head) by one wave.
+__device__ __forceinline__ void merge_partitions(const MqParams& p, int64_t rh, int Lk, int lane) {
   Lk = min(Lk, key_capacity(p));
   if (Lk <= 0) return;
   const int n_parts = (Lk + p.part_tokens - 1) / p.part_tokens;
@@ -612,6 +592,30 @@ __global__ __launch_bounds__(256) void mq_reduce_kernel(MqParams p) {
   *reinterpret_cast<uint32_t*>(p.out + rh * kHeadDim + 2 * lane) = w;
 }
 
+// Decode mode: one wave per (sequence, head).
+__global__ __launch_bounds__(256) void mq_reduce_kernel(MqParams p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t rh = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (rh >= (int64_t)p.num_seqs * p.Hq) return;
+  merge_partitions(p, rh, p.context_lens[rh / p.Hq], lane);
+}
+
+// Varlen mode: one workgroup per sequence; only short-query sequences (the
+// ones the split-KV kernel served) have partitions to merge.
+__global__ __launch_bounds__(256) void mq_reduce_varlen_kernel(MqParams p) {
+  const int seq = blockIdx.x;
+  const int row0 = p.cu_q[seq];
+  const int Lq = p.cu_q[seq + 1] - row0;
+  if (Lq <= 0 || Lq > p.mq_max_q) return;
+  const int Lk = p.cu_k[seq + 1] - p.cu_k[seq];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int idx = wave; idx < Lq * p.Hq; idx += 4) {
+    const int64_t row = (int64_t)row0 + idx / p.Hq;
+    if (row >= p.q_rows) break;
+    merge_partitions(p, row * p.Hq + idx % p.Hq, Lk, lane);
+  }
+}
+
 hipError_t launch_paged_mq(const MqParams& p, int ncb, hipStream_t stream) {
   if (p.num_seqs == 0) return hipSuccess;
   const int hg = (p.Hkv % 2 == 0) ? 2 : 1;  // kv heads per workgroup
@@ -627,8 +631,12 @@ hipError_t launch_paged_mq(const MqParams& p, int ncb, hipStream_t stream) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (p.max_parts > 1) {
-    const int64_t waves = p.q_rows * p.Hq;
-    hipLaunchKernelGGL(mq_reduce_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream, p);
+    if (p.cu_q != nullptr) {
+      hipLaunchKernelGGL(mq_reduce_varlen_kernel, dim3((unsigned)p.num_seqs), dim3(256), 0, stream, p);
+    } else {
+      const int64_t waves = (int64_t)p.num_seqs * p.Hq;
+      hipLaunchKernelGGL(mq_reduce_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream, p);
+    }
     e = hipGetLastError();
   }
   return e;
