@@ -31,8 +31,9 @@
 // kv tokens (i%4) + 8(i/4) + 4h of each 32-token row block, so the PV
 // operand for k-step ks is simply p[ks/2][8(ks%2) .. +8) once V^T is stored
 // with bits 2 and 3 of the token index swapped inside each 16-token step.
-// The V^T rows also XOR their 16-byte chunks with bits 3..5 of the dim
-// index, which spreads the transposing stores over all banks.  The causal
+// The V^T rows XOR their 16-byte chunks with bits 5..6 of the dim index and
+// the V staging lanes are arranged so the transposing stores, the K stores
+// and the MFMA operand reads are all free of LDS bank conflicts.  The causal
 // mask is applied in registers only on tiles that cross the diagonal (or
 // the end of the sequence); tiles wholly above a wave's rows are skipped.
 // The kernel is register-budgeted for two waves per SIMD.
@@ -64,9 +65,23 @@ __device__ __forceinline__ int v_pos(int t) {
   return (t & ~12) | (b2 << 3) | (b3 << 2);
 }
 
-// 16-byte chunk swizzle of V^T row `dim`: XOR of the column (in bf16) with
-// 8 * bits 3..5 of the dim.  Keeps 8-element chunks intact.
-__device__ __forceinline__ int v_swz(int dim) { return ((dim >> 3) & 7) << 3; }
+// Chunk swizzle of V^T row `dim`: XOR of the column (in bf16) with 16 *
+// bits 5..6 of the dim.  It is constant across the 32 rows one MFMA operand
+// read touches (those rows are conflict-free as they are: 144-byte pitch),
+// and separates the dim blocks a staging store group writes.  Keeps 8-element
+// chunks intact.
+__device__ __forceinline__ int v_swz(int dim) { return ((dim >> 5) & 3) << 4; }
+
+// One 8-byte LDS store, kept as its own instruction (the compiler would pair
+// adjacent rows into ds_write2_b64, whose two halves collide in the banks).
+// Completion is waited for explicitly before the barrier that publishes it.
+__device__ __forceinline__ void lds_store8(const uint16_t* p, u32x2 v) {
+  const uint32_t a = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint16_t*)p;
+  asm volatile("ds_write_b64 %0, %1" ::"v"(a), "v"(v));
+}
+
+// s_waitcnt lgkmcnt(0): every LDS access of this wave has completed.
+__device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xc07f); }
 
 struct ItemGeom {
   int q_start, Lq, k_start, Lk, c;
@@ -205,10 +220,17 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillParams p,
   const int64_t rs = (int64_t)p.Hkv * kHeadDim;  // bytes between token rows
 
   // ---- per-thread load / staging geometry ------------------------------------
+  // K: thread t loads and stages 16 fp8 of rows t/8 and t/8 + 32.
+  // V: thread t loads dims [8*dg, +8) of tokens 4*tg + e.  Inside each
+  // 16-lane group the lanes span 4 dim blocks (bits 5..6 of the dim, which
+  // pick the chunk swizzle) x 4 token groups, so the group's transposing
+  // stores (one dim row, 4 tokens each) land on 16 distinct bank pairs;
+  // each load instruction still covers 4 whole rows.
   const int k_row = tid >> 3;                       // K rows k_row and k_row + 32
   const int k_byte = 16 * (tid & 7);
-  const int v_tg = tid >> 4;                        // V tokens 4*v_tg + e
-  const int v_byte = 8 * (tid & 15);                // V dims [v_byte, +8)
+  const int v_q = tid & 15, v_g = (tid >> 4) & 3;
+  const int v_tg = (v_q & 3) + 4 * (tid >> 6);                          // tokens 4*v_tg + e
+  const int v_byte = 8 * (4 * (v_q >> 2) + (v_g & 1) + 2 * (v_g >> 1));  // dims [v_byte, +8)
   const uint32_t k_off0 = (uint32_t)(k_row * rs + k_byte);
   const uint32_t k_off1 = (uint32_t)((k_row + 32) * rs + k_byte);
   const uint32_t v_off = (uint32_t)(4 * v_tg * rs + v_byte);
@@ -248,6 +270,9 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillParams p,
   auto stage_tile = [&](const TileRegs& tr, int b) {
     uint16_t* kb = lds + b * kBufElems;
     uint16_t* vb = kb + kKElems;
+    // Lanes 4..7 of each row store their high 16 bytes first, so each
+    // store instruction's 8-lane groups cover all banks of the row.
+    const bool swap_halves = (tid & 4) != 0;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const u32x4 w = tr.k[i];
@@ -257,8 +282,9 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillParams p,
       hi.x = fp8x2_to_bf16x2<false>(w.z); hi.y = fp8x2_to_bf16x2<true>(w.z);
       hi.z = fp8x2_to_bf16x2<false>(w.w); hi.w = fp8x2_to_bf16x2<true>(w.w);
       uint16_t* kd = kb + (k_row + 32 * i) * kKPitch + k_byte;
-      *reinterpret_cast<u32x4*>(kd) = lo;
-      *reinterpret_cast<u32x4*>(kd + 8) = hi;
+      const u32x4 first = swap_halves ? hi : lo, second = swap_halves ? lo : hi;
+      *reinterpret_cast<u32x4*>(kd + (swap_halves ? 8 : 0)) = first;
+      *reinterpret_cast<u32x4*>(kd + (swap_halves ? 0 : 8)) = second;
     }
     // V: transpose 4 tokens x 8 dims; one 8-byte store (4 tokens) per dim.
     const int pos = v_pos(4 * v_tg);  // tokens 4tg..4tg+3 stay contiguous
@@ -279,7 +305,7 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillParams p,
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int dim = v_byte + 4 * half + e;
-        *reinterpret_cast<u32x2*>(vb + dim * kVPitch + (pos ^ v_swz(dim))) = fp8x4_to_bf16x4(tt[e]);
+        lds_store8(vb + dim * kVPitch + (pos ^ v_swz(dim)), fp8x4_to_bf16x4(tt[e]));
       }
     }
   };
@@ -385,15 +411,18 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillParams p,
     load_tile(t0, ra);
     load_tile(t0 + 1 < t1 ? t0 + 1 : n_tiles, rb);
     stage_tile(ra, 0);
+    wait_lds();
     __syncthreads();
     for (int t = t0; t < t1; t += 2) {
       load_tile(t + 2 < t1 ? t + 2 : n_tiles, ra);
       compute_tile(t, 0);
       stage_tile(rb, 1);
+      wait_lds();
       __syncthreads();
       load_tile(t + 3 < t1 ? t + 3 : n_tiles, rb);
       if (t + 1 < t1) compute_tile(t + 1, 1);
       stage_tile(ra, 0);
+      wait_lds();
       __syncthreads();
     }
   }
