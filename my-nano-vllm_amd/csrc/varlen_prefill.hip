@@ -319,19 +319,35 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillParams p,
     const uint16_t* vb = kb + kKElems;
 
     // ---- S^T = K . Q^T ------------------------------------------------------
+    // The two row blocks' MFMA chains are interleaved (step i: k-step i/2 of
+    // row block i%2) and each K operand is read from LDS four steps before
+    // its MFMA, so the LDS latency hides behind the MFMAs in flight.
     f32x16 s[2];
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      f32x16 a;
+    for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) a[i] = 0.f;
-      const uint16_t* kr = kb + (32 * rb + col) * kKPitch + 8 * h;
+      for (int i = 0; i < 16; ++i) s[rb][i] = 0.f;
+    {
+      const uint16_t* kr = kb + col * kKPitch + 8 * h;
+      auto kaddr = [&](int i) { return kr + (i & 1) * 32 * kKPitch + 16 * (i >> 1); };
+      u32x4 pre[4];
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
-        const bf16x8 kop = as_bf16x8(*reinterpret_cast<const u32x4*>(kr + 16 * ks));
-        a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, qop[ks], a, 0, 0, 0);
+      for (int i = 0; i < 4; ++i) pre[i] = *reinterpret_cast<const u32x4*>(kaddr(i));
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const u32x4 cur = pre[i & 3];
+        if (i + 4 < 16) pre[i & 3] = *reinterpret_cast<const u32x4*>(kaddr(i + 4));
+        s[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(cur), qop[i >> 1], s[i & 1], 0, 0, 0);
       }
-      s[rb] = a;
+      // Keep that order through scheduling: 4 LDS reads, then MFMA / read
+      // pairs, then the last 4 MFMAs.
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+      for (int i = 0; i < 12; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
     }
 
     // ---- online softmax (row = query column of this lane) -----------------
@@ -376,20 +392,38 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillParams p,
     l_run += ps;
 
     // ---- O^T += V^T . P^T -----------------------------------------------------
+    // MFMA i = (k-step i/4, dim block i%4); each V^T operand is read from LDS
+    // four MFMAs ahead (same scheme as S^T).
+    {
+      auto vaddr = [&](int i) {
+        const int ks = i >> 2, d = 32 * (i & 3) + col;
+        return vb + d * kVPitch + ((16 * ks + 8 * h) ^ v_swz(d));
+      };
+      u32x4 pre[4];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int rb = ks >> 1, base = 8 * (ks & 1);
-      const bf16x8 pop = as_bf16x8(pack_bf16x2(s[rb][base + 0], s[rb][base + 1]),
-                                   pack_bf16x2(s[rb][base + 2], s[rb][base + 3]),
-                                   pack_bf16x2(s[rb][base + 4], s[rb][base + 5]),
-                                   pack_bf16x2(s[rb][base + 6], s[rb][base + 7]));
+      for (int i = 0; i < 4; ++i) pre[i] = *reinterpret_cast<const u32x4*>(vaddr(i));
+      bf16x8 pop;
 #pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const int d = 32 * db + col;
-        const bf16x8 vop = as_bf16x8(*reinterpret_cast<const u32x4*>(
-            vb + d * kVPitch + ((16 * ks + 8 * h) ^ v_swz(d))));
-        acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop, pop, acc[db], 0, 0, 0);
+      for (int i = 0; i < 16; ++i) {
+        const int ks = i >> 2;
+        if ((i & 3) == 0) {
+          const int rb = ks >> 1, base = 8 * (ks & 1);
+          pop = as_bf16x8(pack_bf16x2(s[rb][base + 0], s[rb][base + 1]),
+                          pack_bf16x2(s[rb][base + 2], s[rb][base + 3]),
+                          pack_bf16x2(s[rb][base + 4], s[rb][base + 5]),
+                          pack_bf16x2(s[rb][base + 6], s[rb][base + 7]));
+        }
+        const u32x4 cur = pre[i & 3];
+        if (i + 4 < 16) pre[i & 3] = *reinterpret_cast<const u32x4*>(vaddr(i + 4));
+        acc[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(cur), pop, acc[i & 3], 0, 0, 0);
       }
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+      for (int i = 0; i < 12; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
     }
   };
 
