@@ -111,7 +111,7 @@ int heads_per_workgroup(int g) {
 int64_t align_up(int64_t n) { return (n + 255) / 256 * 256; }
 
 // Prefill kernel geometry for G query heads per kv head.
-int prefill_bm(int g) { return 128 / heads_per_workgroup(g); }
+int prefill_bm(int g) { return 32 * nvamd::kPrefillWaves / heads_per_workgroup(g); }
 
 // Bytes of the prefill work list (0 when every sequence takes the
 // short-query path).
@@ -321,7 +321,7 @@ int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, con
     p.Hkv = num_kv_heads;
     p.G = G;
     p.GW = heads_per_workgroup(G);
-    p.BM = 128 / p.GW;
+    p.BM = prefill_bm(G);
     p.n_hgroups = G / p.GW;
     p.n_mblocks = (int)ceil_div(max_seqlen_q, p.BM);
     p.block_size = paged ? block_size : 64;

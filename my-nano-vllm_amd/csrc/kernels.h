@@ -29,6 +29,9 @@ struct MqParams {
   float scale_log2;
 };
 
+// Waves per prefill workgroup: each owns 32 query rows of one head.
+constexpr int kPrefillWaves = 8;
+
 // Varlen causal prefill (long query blocks).
 struct PrefillParams {
   const uint16_t* q;
@@ -44,7 +47,7 @@ struct PrefillParams {
   int num_seqs;
   int Hq, Hkv, G;
   int GW;         // query heads per workgroup
-  int BM;         // query tokens per workgroup (128 / GW)
+  int BM;         // query tokens per workgroup (32 * kPrefillWaves / GW)
   int n_hgroups;  // G / GW
   int n_mblocks;  // ceil(max_seqlen_q / BM)
   int block_size;

@@ -8,21 +8,22 @@
 // [cu_k[s], cu_k[s+1]) when block_tables is NULL (fp8_attention.py:254-278).
 //
 // Work item = (sequence, m-block of BM query tokens) x (kv head, group of GW
-// query heads sharing it).  A workgroup is 4 waves = 128 query rows = GW
+// query heads sharing it).  A workgroup is 8 waves = 256 query rows = GW
 // heads x BM tokens; wave w owns 32 rows: head (w % GW), tokens
 // [m0 + 32*(w / GW), +32).  prefill_schedule_kernel first orders the items
 // by decreasing number of KV tiles (a counting sort on the device), and the
 // grid walks that list with the kv-head group varying fastest, so the
 // longest items start first and short ones fill the tail.
 //
-// K/V stream in 64-token tiles.  Each thread loads its share of an FP8 tile
-// into registers two tiles ahead (bounded raw buffer loads: rows past the
-// sequence read as zero, so every iteration issues the same loads and the
-// compiler's wait counts stay exact), converts it to bf16 (exact) and
+// K/V stream in 64-token tiles, K one tile ahead of V.  Waves 0..3 load and
+// stage K tiles, waves 4..7 V tiles: each thread loads its share of an FP8
+// tile into registers two steps ahead (bounded raw buffer loads: rows past
+// the sequence read as zero, so every iteration issues the same loads and
+// the compiler's wait counts stay exact), converts it to bf16 (exact) and
 // stages it in one of two LDS buffers -- K as [token][dim], V transposed as
 // [dim][token] -- while the waves compute the other buffer.  One barrier
-// per tile.  Each K load instruction fetches whole 128-byte rows (8 lanes
-// per row), each V load instruction 4 whole rows.
+// per tile.  Each K load instruction fetches 8 rows (8 lanes per row), each
+// V load instruction 4 whole rows.
 //
 // Per tile a wave computes with v_mfma_f32_32x32x16_bf16 (fp32 accumulate):
 //     S^T[kv][q] = K[kv][:] . Q[q][:]          2 row blocks x 8 k-steps
@@ -36,7 +37,9 @@
 // and the MFMA operand reads are all free of LDS bank conflicts.  The causal
 // mask is applied in registers only on tiles that cross the diagonal (or
 // the end of the sequence); tiles wholly above a wave's rows are skipped.
-// The kernel is register-budgeted for two waves per SIMD.
+// Step t of a wave runs the softmax of S_t with the MFMAs of S_{t+1}
+// interleaved between its exponentials, then O += P_t V_t.  The kernel is
+// register-budgeted for two waves per SIMD (one workgroup per CU).
 #include "fp8_common.h"
 #include "kernels.h"
 
@@ -49,13 +52,16 @@ constexpr int kKPitch = kHeadDim + 8;         // bf16 per K row in LDS (272 B)
 constexpr int kVPitch = kBN + 8;              // bf16 per V^T row in LDS (144 B)
 constexpr int kKElems = kBN * kKPitch;        // 8704
 constexpr int kVElems = kHeadDim * kVPitch;   // 9216
-constexpr int kBufElems = kKElems + kVElems;  // 17920 bf16 = 35840 B per buffer
+constexpr int kBufElems = kKElems + kVElems;  // 17920 bf16 = 35840 B per K + V pair
 constexpr int kBtWindow = 64;                 // block-table entries held in one register
 constexpr int kCostBuckets = 1024;            // schedule sort resolution (tiles)
 
+// One staging thread's share of a K or V tile (see the staging geometry in
+// the kernel): K rows s/8 (r[0], r[1]) and s/8 + 32 (r[2], r[3]), bytes
+// [16*(s%8), +16) of each, as two 8-byte halves in store order; or 8 fp8
+// (one dim group) of each of 4 tokens.
 struct TileRegs {
-  u32x4 k[2];   // 16 B of K rows (tid/8) and (tid/8 + 32): bytes [16*(tid%8), +16)
-  u32x2 v[4];   // 8 B (dims [8*(tid%16), +8)) of tokens 4*(tid/16) + e
+  u32x2 r[4];
 };
 
 // position of token t (0..63) inside the transposed V tile before the chunk
@@ -72,12 +78,15 @@ __device__ __forceinline__ int v_pos(int t) {
 // chunks intact.
 __device__ __forceinline__ int v_swz(int dim) { return ((dim >> 5) & 3) << 4; }
 
-// One 8-byte LDS store, kept as its own instruction (the compiler would pair
-// adjacent rows into ds_write2_b64, whose two halves collide in the banks).
-// Completion is waited for explicitly before the barrier that publishes it.
+// One 8-byte LDS store to p + OFF bytes, kept as its own instruction (the
+// compiler would pair adjacent rows into ds_write2_b64, whose two halves
+// collide in the banks).  Completion is waited for explicitly before the
+// barrier that publishes it.
+template <int OFF>
 __device__ __forceinline__ void lds_store8(const uint16_t* p, u32x2 v) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds_write_b64 offset is 16 bits");
   const uint32_t a = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint16_t*)p;
-  asm volatile("ds_write_b64 %0, %1" ::"v"(a), "v"(v));
+  asm volatile("ds_write_b64 %0, %1 offset:%2" ::"v"(a), "v"(v), "i"(OFF));
 }
 
 // s_waitcnt lgkmcnt(0): every LDS access of this wave has completed.
@@ -170,7 +179,8 @@ __global__ __launch_bounds__(256) void prefill_schedule_kernel(PrefillParams p, 
 // ---------------------------------------------------------------------------
 // Main kernel
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillParams p, const int2* __restrict__ items) {
+__global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(PrefillParams p,
+                                                                              const int2* __restrict__ items) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kBufElems];
 
   // blockIdx.x = item * n_groups + group: the kv-head group varies fastest.
@@ -220,28 +230,35 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillParams p,
   const int64_t rs = (int64_t)p.Hkv * kHeadDim;  // bytes between token rows
 
   // ---- per-thread load / staging geometry ------------------------------------
-  // K: thread t loads and stages 16 fp8 of rows t/8 and t/8 + 32.
-  // V: thread t loads dims [8*dg, +8) of tokens 4*tg + e.  Inside each
+  // Waves 0..3 load and stage K tiles, waves 4..7 V tiles; s = tid % 256.
+  // K: thread s loads and stages 16 fp8 of rows s/8 and s/8 + 32.
+  // V: thread s loads dims [8*dg, +8) of tokens 4*tg + e.  Inside each
   // 16-lane group the lanes span 4 dim blocks (bits 5..6 of the dim, which
   // pick the chunk swizzle) x 4 token groups, so the group's transposing
   // stores (one dim row, 4 tokens each) land on 16 distinct bank pairs;
   // each load instruction still covers 4 whole rows.
-  const int k_row = tid >> 3;                       // K rows k_row and k_row + 32
-  const int k_byte = 16 * (tid & 7);
-  const int v_q = tid & 15, v_g = (tid >> 4) & 3;
-  const int v_tg = (v_q & 3) + 4 * (tid >> 6);                          // tokens 4*v_tg + e
+  const bool k_role = wave < 4;
+  const int stid = tid & 255;
+  const int k_row = stid >> 3;                      // K rows k_row and k_row + 32
+  const int k_byte = 16 * (stid & 7);
+  const int v_q = stid & 15, v_g = (stid >> 4) & 3;
+  const int v_tg = (v_q & 3) + 4 * (stid >> 6);                         // tokens 4*v_tg + e
   const int v_byte = 8 * (4 * (v_q >> 2) + (v_g & 1) + 2 * (v_g >> 1));  // dims [v_byte, +8)
-  const uint32_t k_off0 = (uint32_t)(k_row * rs + k_byte);
-  const uint32_t k_off1 = (uint32_t)((k_row + 32) * rs + k_byte);
+  // Lanes 4..7 of each K row store (and so load) their high 8 fp8 first,
+  // so each store instruction's 8-lane groups cover all banks of the row.
+  const int k_first = (stid & 4) ? 8 : 0;
+  const uint32_t k_off0 = (uint32_t)(k_row * rs + k_byte + k_first);
+  const uint32_t k_off1 = (uint32_t)((k_row + 32) * rs + k_byte + k_first);
   const uint32_t v_off = (uint32_t)(4 * v_tg * rs + v_byte);
   const uint32_t urs = (uint32_t)rs;
 
   // Block-table window: lane l holds entry win_base + l (paged layout).
   int bt_lane = 0, win_base = 0;
 
-  // Issues the loads of tile t into tr.  Tiles past the item (or with an
-  // invalid block) get zero-length descriptors: the loads read nothing.
-  auto load_tile = [&](int t, TileRegs& tr) {
+  // Buffer descriptor of tile t of this wave's role (K or V).  Tiles past
+  // the item (or with an invalid block) get zero-length descriptors: their
+  // loads read nothing.
+  auto tile_rsrc = [&](int t) {
     const int kv0 = t * kBN;
     int nvalid = (t < n_tiles) ? min(kBN, Lk - kv0) : 0;
     int64_t row0 = 0;
@@ -258,42 +275,48 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillParams p,
     if (nvalid == 0) row0 = 0;
     const int64_t base = (row0 * p.Hkv + g) * kHeadDim;
     const uint32_t nbytes = (uint32_t)(nvalid * rs);
-    const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.k + base, nbytes);
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.v + base, nbytes);
-    tr.k[0] = buf_load16(rk, k_off0);
-    tr.k[1] = buf_load16(rk, k_off1);
+    return make_rsrc((k_role ? p.k : p.v) + base, nbytes);
+  };
+  // Loads this thread's share of tile t of its role: K tile t (K waves) or
+  // V tile tv (V waves).
+  auto load = [&](int t, int tv, TileRegs& r) {
+    const __amdgpu_buffer_rsrc_t rs_ = tile_rsrc(k_role ? t : tv);
+    if (k_role) {
+      r.r[0] = buf_load8(rs_, k_off0);
+      r.r[1] = buf_load8(rs_, k_off0 ^ 8u);
+      r.r[2] = buf_load8(rs_, k_off1);
+      r.r[3] = buf_load8(rs_, k_off1 ^ 8u);
+    } else {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) tr.v[e] = buf_load8(rv, v_off + (uint32_t)e * urs);
+      for (int e = 0; e < 4; ++e) r.r[e] = buf_load8(rs_, v_off + (uint32_t)e * urs);
+    }
   };
 
-  // Converts tile registers to bf16 and writes LDS buffer `b`.
-  auto stage_tile = [&](const TileRegs& tr, int b) {
-    uint16_t* kb = lds + b * kBufElems;
-    uint16_t* vb = kb + kKElems;
-    // Lanes 4..7 of each row store their high 16 bytes first, so each
-    // store instruction's 8-lane groups cover all banks of the row.
-    const bool swap_halves = (tid & 4) != 0;
+  // Converts a K tile share to bf16 and writes it to K buffer kb.
+  const int k_lds[2] = {k_row * kKPitch + k_byte + k_first, k_row * kKPitch + k_byte + (k_first ^ 8)};
+  auto stage_k = [&](const TileRegs& kr, uint16_t* kb) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const u32x4 w = tr.k[i];
-      u32x4 lo, hi;
-      lo.x = fp8x2_to_bf16x2<false>(w.x); lo.y = fp8x2_to_bf16x2<true>(w.x);
-      lo.z = fp8x2_to_bf16x2<false>(w.y); lo.w = fp8x2_to_bf16x2<true>(w.y);
-      hi.x = fp8x2_to_bf16x2<false>(w.z); hi.y = fp8x2_to_bf16x2<true>(w.z);
-      hi.z = fp8x2_to_bf16x2<false>(w.w); hi.w = fp8x2_to_bf16x2<true>(w.w);
-      uint16_t* kd = kb + (k_row + 32 * i) * kKPitch + k_byte;
-      const u32x4 first = swap_halves ? hi : lo, second = swap_halves ? lo : hi;
-      *reinterpret_cast<u32x4*>(kd + (swap_halves ? 8 : 0)) = first;
-      *reinterpret_cast<u32x4*>(kd + (swap_halves ? 0 : 8)) = second;
+    for (int i = 0; i < 4; ++i) {
+      const u32x2 w = kr.r[i];
+      u32x4 o;
+      o.x = fp8x2_to_bf16x2<false>(w.x); o.y = fp8x2_to_bf16x2<true>(w.x);
+      o.z = fp8x2_to_bf16x2<false>(w.y); o.w = fp8x2_to_bf16x2<true>(w.y);
+      *reinterpret_cast<u32x4*>(kb + k_lds[i & 1] + (i >> 1) * 32 * kKPitch) = o;
     }
-    // V: transpose 4 tokens x 8 dims; one 8-byte store (4 tokens) per dim.
-    const int pos = v_pos(4 * v_tg);  // tokens 4tg..4tg+3 stay contiguous
+  };
+  // Transposes a V tile share (4 tokens x 8 dims) to bf16 and writes it to
+  // V^T buffer vb: one 8-byte store (4 tokens) per dim.
+  // Dims v_byte..v_byte+7 share one chunk swizzle (v_byte is a multiple of
+  // 8), so the 8 stores are one address plus constant offsets.
+  const int v_lds = v_byte * kVPitch + (v_pos(4 * v_tg) ^ v_swz(v_byte));  // tokens 4tg..4tg+3 stay contiguous
+  auto stage_v = [&](const TileRegs& vr, uint16_t* vb) {
+    uint16_t* vd = vb + v_lds;
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
-      const uint32_t a = half ? tr.v[0].y : tr.v[0].x;
-      const uint32_t bb = half ? tr.v[1].y : tr.v[1].x;
-      const uint32_t cc = half ? tr.v[2].y : tr.v[2].x;
-      const uint32_t d = half ? tr.v[3].y : tr.v[3].x;
+      const uint32_t a = half ? vr.r[0].y : vr.r[0].x;
+      const uint32_t bb = half ? vr.r[1].y : vr.r[1].x;
+      const uint32_t cc = half ? vr.r[2].y : vr.r[2].x;
+      const uint32_t d = half ? vr.r[3].y : vr.r[3].x;
       const uint32_t x01 = __builtin_amdgcn_perm(a, bb, 0x01050004u);   // [a0 b0 a1 b1]
       const uint32_t y01 = __builtin_amdgcn_perm(cc, d, 0x01050004u);   // [c0 d0 c1 d1]
       const uint32_t x23 = __builtin_amdgcn_perm(a, bb, 0x03070206u);   // [a2 b2 a3 b3]
@@ -302,75 +325,106 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillParams p,
                               __builtin_amdgcn_perm(x01, y01, 0x03020706u),   // [a1 b1 c1 d1]
                               __builtin_amdgcn_perm(x23, y23, 0x01000504u),   // [a2 b2 c2 d2]
                               __builtin_amdgcn_perm(x23, y23, 0x03020706u)};  // [a3 b3 c3 d3]
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int dim = v_byte + 4 * half + e;
-        lds_store8(vb + dim * kVPitch + (pos ^ v_swz(dim)), fp8x4_to_bf16x4(tt[e]));
+      constexpr int kRow = 2 * kVPitch;  // bytes per V^T row
+      if (half == 0) {
+        lds_store8<0 * kRow>(vd, fp8x4_to_bf16x4(tt[0]));
+        lds_store8<1 * kRow>(vd, fp8x4_to_bf16x4(tt[1]));
+        lds_store8<2 * kRow>(vd, fp8x4_to_bf16x4(tt[2]));
+        lds_store8<3 * kRow>(vd, fp8x4_to_bf16x4(tt[3]));
+      } else {
+        lds_store8<4 * kRow>(vd, fp8x4_to_bf16x4(tt[0]));
+        lds_store8<5 * kRow>(vd, fp8x4_to_bf16x4(tt[1]));
+        lds_store8<6 * kRow>(vd, fp8x4_to_bf16x4(tt[2]));
+        lds_store8<7 * kRow>(vd, fp8x4_to_bf16x4(tt[3]));
       }
     }
   };
 
-  // Attention over tile t (LDS buffer b) for this wave's 32 rows.
-  auto compute_tile = [&](int t, int b) {
-    const int kv0 = t * kBN;
-    if (kv0 > c + m0w + 31) return;  // wholly above this wave's causal diagonal
-    const bool need_mask = (kv0 + kBN - 1 > c + m0w) || (kv0 + kBN > Lk);
-    const uint16_t* kb = lds + b * kBufElems;
-    const uint16_t* vb = kb + kKElems;
-
-    // ---- S^T = K . Q^T ------------------------------------------------------
-    // The two row blocks' MFMA chains are interleaved (step i: k-step i/2 of
-    // row block i%2) and each K operand is read from LDS four steps before
-    // its MFMA, so the LDS latency hides behind the MFMAs in flight.
-    f32x16 s[2];
+  // S^T = K . Q^T of one tile (K buffer kb).  The two row blocks' MFMA
+  // chains are interleaved (step i: k-step i/2 of row block i%2); each K
+  // operand is read from LDS four steps before its MFMA.  after(i) runs
+  // behind MFMA i: vector work of another tile that fills the matrix pipe's
+  // shadow.
+  auto qk_mfma = [&](const uint16_t* kb, f32x16 (&s)[2], auto&& after) {
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) s[rb][i] = 0.f;
-    {
-      const uint16_t* kr = kb + col * kKPitch + 8 * h;
-      auto kaddr = [&](int i) { return kr + (i & 1) * 32 * kKPitch + 16 * (i >> 1); };
-      u32x4 pre[4];
+    const uint16_t* kr = kb + col * kKPitch + 8 * h;
+    auto kaddr = [&](int i) { return kr + (i & 1) * 32 * kKPitch + 16 * (i >> 1); };
+    u32x4 pre[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) pre[i] = *reinterpret_cast<const u32x4*>(kaddr(i));
+    for (int i = 0; i < 4; ++i) pre[i] = *reinterpret_cast<const u32x4*>(kaddr(i));
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const u32x4 cur = pre[i & 3];
-        if (i + 4 < 16) pre[i & 3] = *reinterpret_cast<const u32x4*>(kaddr(i + 4));
-        s[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(cur), qop[i >> 1], s[i & 1], 0, 0, 0);
-      }
-      // Keep that order through scheduling: 4 LDS reads, then MFMA / read
-      // pairs, then the last 4 MFMAs.
-      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#pragma unroll
-      for (int i = 0; i < 12; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    for (int i = 0; i < 16; ++i) {
+      const u32x4 cur = pre[i & 3];
+      if (i + 4 < 16) pre[i & 3] = *reinterpret_cast<const u32x4*>(kaddr(i + 4));
+      s[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(cur), qop[i >> 1], s[i & 1], 0, 0, 0);
+      after(i);
     }
+  };
 
-    // ---- online softmax (row = query column of this lane) -----------------
-    // The maximum is taken over raw scores (scale > 0), the exponent is
-    // exp2(s * scale_log2 - m) with m in log2 units.
-    if (need_mask) {
-      const int lim = c + tq;  // last visible key
+  // O^T += V^T . P^T for one tile (V^T in buffer vb): MFMA i = (k-step i/4,
+  // dim block i%4); each V^T operand is read four MFMAs ahead.
+  auto pv = [&](const bf16x8 (&pp)[4], const uint16_t* vb) {
+    auto vaddr = [&](int i) {
+      const int ks = i >> 2, d = 32 * (i & 3) + col;
+      return vb + d * kVPitch + ((16 * ks + 8 * h) ^ v_swz(d));
+    };
+    u32x4 pre[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pre[i] = *reinterpret_cast<const u32x4*>(vaddr(i));
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const u32x4 cur = pre[i & 3];
+      if (i + 4 < 16) pre[i & 3] = *reinterpret_cast<const u32x4*>(vaddr(i + 4));
+      acc[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(cur), pp[i >> 2], acc[i & 3], 0, 0, 0);
+    }
+    // keep the reads four MFMAs ahead (the scheduler would otherwise sink
+    // them next to their MFMAs to save registers)
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (i < 12) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+  };
+
+  // One pipeline step for tile t of this wave: softmax of S_t (already in
+  // s_cur), O^T += V^T . P^T from V buffer vb, and S_{t+1} = K . Q^T from K
+  // buffer kb_next into s_next.  The S_{t+1} MFMAs are issued between the
+  // exponentials of tile t, so the matrix and vector pipes work on different
+  // tiles at the same time.  `loads` issues the step's global loads after the
+  // exponentials, where S_t is dead and the registers they fill are free;
+  // every wave issues them, since the whole workgroup stages each tile.
+  auto step = [&](int t, bool run, f32x16 (&s_cur)[2], f32x16 (&s_next)[2], const uint16_t* kb_next,
+                  const uint16_t* vb, auto&& loads) {
+    const int kv0 = t * kBN;
+    // not run, or tile t (and every later one) above this wave's diagonal:
+    // nothing but the loads
+    const bool active = run && kv0 <= c + m0w + 31;
+    bf16x8 pop[4];
+    if (active) {
+    if ((kv0 + kBN - 1 > c + m0w) || (kv0 + kBN > Lk)) {
+      // key kv0 + 4h + off is visible iff off < rem (keys up to c + tq, below Lk)
+      const int rem = min(c + tq + 1, Lk) - kv0 - 4 * h;
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int j = kv0 + 32 * rb + (i & 3) + 8 * (i >> 2) + 4 * h;
-          s[rb][i] = (j <= lim && j < Lk) ? s[rb][i] : -INFINITY;
+          const int off = 32 * rb + (i & 3) + 8 * (i >> 2);
+          s_cur[rb][i] = (off < rem) ? s_cur[rb][i] : -INFINITY;
         }
     }
+    // The maximum is taken over raw scores (scale > 0); exponents are
+    // exp2(s * scale_log2 - m) with m in log2 units.
     float mx = -INFINITY;
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[rb][i]);
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s_cur[rb][i]);
     mx = fmaxf(mx, shfl_xor_f32(mx, 32)) * p.scale_log2;
-    // Lazy rescale (see kLazyRescaleLog2).
-    const bool grow = mx > m_run + kLazyRescaleLog2;
+    const bool grow = mx > m_run + kLazyRescaleLog2;  // lazy rescale (see kLazyRescaleLog2)
     if (wave_any(grow)) {
       const float m_new = grow ? mx : m_run;
       const float alpha = grow ? fast_exp2(m_run - m_new) : 1.f;
@@ -380,59 +434,50 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillParams p,
       for (int db = 0; db < 4; ++db) acc[db] *= alpha;
     }
     const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
-    float ps = 0.f;
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float e = fast_exp2(__builtin_fmaf(s[rb][i], p.scale_log2, -m_use));
-        s[rb][i] = e;
-        ps += e;
-      }
-    l_run += ps;
 
-    // ---- O^T += V^T . P^T -----------------------------------------------------
-    // MFMA i = (k-step i/4, dim block i%4); each V^T operand is read from LDS
-    // four MFMAs ahead (same scheme as S^T).
-    {
-      auto vaddr = [&](int i) {
-        const int ks = i >> 2, d = 32 * (i & 3) + col;
-        return vb + d * kVPitch + ((16 * ks + 8 * h) ^ v_swz(d));
-      };
-      u32x4 pre[4];
+    // exponentials of tile t, two behind each S_{t+1} MFMA: element n of
+    // S_t is s_cur[n / 16][n % 16]; word i of the P^T operands holds
+    // elements 2i and 2i + 1.
+    uint32_t pw[16];
+    float ps0 = 0.f, ps1 = 0.f;
+    qk_mfma(kb_next, s_next, [&](int i) {
+      const int rb = i >> 3, n = (2 * i) & 15;
+      const float e0 = fast_exp2(__builtin_fmaf(s_cur[rb][n], p.scale_log2, -m_use));
+      const float e1 = fast_exp2(__builtin_fmaf(s_cur[rb][n + 1], p.scale_log2, -m_use));
+      ps0 += e0;
+      ps1 += e1;
+      pw[i] = pack_bf16x2(e0, e1);
+    });
+    l_run += ps0 + ps1;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) pre[i] = *reinterpret_cast<const u32x4*>(vaddr(i));
-      bf16x8 pop;
+    for (int ks = 0; ks < 4; ++ks) pop[ks] = as_bf16x8(pw[4 * ks], pw[4 * ks + 1], pw[4 * ks + 2], pw[4 * ks + 3]);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int ks = i >> 2;
-        if ((i & 3) == 0) {
-          const int rb = ks >> 1, base = 8 * (ks & 1);
-          pop = as_bf16x8(pack_bf16x2(s[rb][base + 0], s[rb][base + 1]),
-                          pack_bf16x2(s[rb][base + 2], s[rb][base + 3]),
-                          pack_bf16x2(s[rb][base + 4], s[rb][base + 5]),
-                          pack_bf16x2(s[rb][base + 6], s[rb][base + 7]));
-        }
-        const u32x4 cur = pre[i & 3];
-        if (i + 4 < 16) pre[i & 3] = *reinterpret_cast<const u32x4*>(vaddr(i + 4));
-        acc[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(cur), pop, acc[i & 3], 0, 0, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#pragma unroll
-      for (int i = 0; i < 12; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (i < 12) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x402, 7, 0);
     }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    loads();
+    __builtin_amdgcn_sched_barrier(0);
+    if (active) pv(pop, vb);
   };
 
   // ---- tile loop, one block-table window at a time -----------------------------
-  // Within a window: tile t is computed from buffer t%2 while tile t+1 is
-  // staged into the other buffer and tile t+2 is loading into registers.
-  // The loop runs whole pairs of tiles and leaves only through its latch (a
-  // phantom last tile is skipped by a uniform branch), so every path into
-  // the loop head has the same loads in flight.
+  // K runs one tile ahead of V.  Step t reads S_{t+1}'s K from K buffer
+  // (t+1)%2 and V_t from V buffer t%2, while K_{t+2} is staged into K buffer
+  // t%2 and V_{t+1} into V buffer (t+1)%2 from registers loaded one step
+  // earlier; the loads issued in step t fetch K_{t+3} and V_{t+2}.  One
+  // barrier per step.  The loop runs whole pairs of steps and leaves only
+  // through its latch; loads past the window read nothing, and steps past it
+  // are skipped by uniform branches, so every path into the loop head has the
+  // same loads in flight.
+  uint16_t* kbuf0 = lds;
+  uint16_t* kbuf1 = lds + kKElems;
+  uint16_t* vbuf0 = lds + 2 * kKElems;
+  uint16_t* vbuf1 = vbuf0 + kVElems;
   const int win_tiles = paged ? kBtWindow * p.block_size / kBN : n_tiles;
   for (int t0 = 0; t0 < n_tiles; t0 += win_tiles) {
     const int t1 = min(n_tiles, t0 + win_tiles);
@@ -441,21 +486,32 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillParams p,
       const int bi = min(win_base + lane, (int)p.bt_stride - 1);
       bt_lane = p.block_tables[(int64_t)seq * p.bt_stride + bi];
     }
+    auto in_win = [&](int t) { return t < t1 ? t : n_tiles; };
     TileRegs ra, rb;
-    load_tile(t0, ra);
-    load_tile(t0 + 1 < t1 ? t0 + 1 : n_tiles, rb);
-    stage_tile(ra, 0);
+    load(t0, t0, ra);
+    if (k_role) {
+      load(in_win(t0 + 1), 0, rb);
+      stage_k(ra, kbuf0);
+      stage_k(rb, kbuf1);
+    } else {
+      stage_v(ra, vbuf0);
+    }
+    load(in_win(t0 + 2), in_win(t0 + 1), ra);
     wait_lds();
     __syncthreads();
+    f32x16 sa[2], sb[2];
+    qk_mfma(kbuf0, sa, [](int) {});
     for (int t = t0; t < t1; t += 2) {
-      load_tile(t + 2 < t1 ? t + 2 : n_tiles, ra);
-      compute_tile(t, 0);
-      stage_tile(rb, 1);
+      step(t, true, sa, sb, kbuf1, vbuf0, [&] { load(in_win(t + 3), in_win(t + 2), rb); });
+      if (k_role) stage_k(ra, kbuf0);
+      else stage_v(ra, vbuf1);
       wait_lds();
       __syncthreads();
-      load_tile(t + 3 < t1 ? t + 3 : n_tiles, rb);
-      if (t + 1 < t1) compute_tile(t + 1, 1);
-      stage_tile(ra, 0);
+      // past the window's last tile: no step, but the loads keep the same
+      // count in flight at the loop head
+      step(t + 1, t + 1 < t1, sb, sa, kbuf0, vbuf1, [&] { load(in_win(t + 4), in_win(t + 3), ra); });
+      if (k_role) stage_k(rb, kbuf1);
+      else stage_v(rb, vbuf0);
       wait_lds();
       __syncthreads();
     }
@@ -494,7 +550,7 @@ hipError_t launch_varlen_prefill(const PrefillParams& p, void* schedule, hipStre
   hipLaunchKernelGGL(prefill_schedule_kernel, dim3(1), dim3(256), 0, stream, p, items, (int)n_items_max);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(varlen_prefill_kernel, dim3((unsigned)n_blocks), dim3(256), 0, stream, p,
+  hipLaunchKernelGGL(varlen_prefill_kernel, dim3((unsigned)n_blocks), dim3(64 * kPrefillWaves), 0, stream, p,
                      (const int2*)items);
   return hipGetLastError();
 }
