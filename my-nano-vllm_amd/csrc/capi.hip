@@ -86,6 +86,27 @@ int64_t partial_bytes(int64_t rows, int64_t heads, int64_t max_parts) {
   return rows * heads * max_parts * kPartialFloats * (int64_t)sizeof(float);
 }
 
+// Balanced (stream-K) decode: used when the caller leaves the partition to
+// the library, the kv heads split into groups of 4 and the batch fits the
+// kernel's in-LDS stage prefix.
+bool use_stream_k(int32_t batch, int32_t num_kv_heads, int32_t part_tokens) {
+  return part_tokens == 0 && num_kv_heads % 4 == 0 && batch <= nvamd::kSkMaxSeqs;
+}
+
+// kv heads per balanced-decode workgroup: whole 1 KiB cache rows when the
+// kv heads come in 8s (each workgroup then reads whole DRAM pages), else 4.
+int stream_k_heads(int32_t num_kv_heads) { return num_kv_heads % 8 == 0 ? 8 : 4; }
+
+int stream_k_wgs(int ncb, int hg) { return device_cu_count() * nvamd::decode_sk_wgs_per_cu(ncb, hg); }
+
+// Workspace of the balanced decode: the stage prefix, then the partial slots.
+int64_t stream_k_prefix_bytes(int32_t batch) { return (((int64_t)batch + 1) * 4 + 255) / 256 * 256; }
+int64_t stream_k_bytes(int32_t batch, int32_t num_kv_heads, int32_t G) {
+  const int ncb = (G + 15) / 16, hg = stream_k_heads(num_kv_heads);
+  return stream_k_prefix_bytes(batch) +
+         (int64_t)stream_k_wgs(ncb, hg) * 2 * hg * G * nvamd::kSkSlotFloats * (int64_t)sizeof(float);
+}
+
 void set_partials(nvamd::MqParams& p, void* workspace) {
   const int64_t n = p.q_rows * p.Hq * p.max_parts;
   p.part_acc = static_cast<float*>(workspace);
@@ -153,6 +174,9 @@ int64_t nvamd_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t n
                                      int32_t max_num_blocks, int32_t block_size, int32_t part_tokens) {
   if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || max_num_blocks <= 0 || block_size <= 0)
     return 0;
+  if (num_heads % num_kv_heads != 0) return 0;
+  if (use_stream_k(batch, num_kv_heads, part_tokens))
+    return stream_k_bytes(batch, num_kv_heads, num_heads / num_kv_heads);
   const int64_t kv_cap = (int64_t)max_num_blocks * block_size;
   const int64_t part = choose_part_tokens((int64_t)batch * kv_head_groups(num_kv_heads), kv_cap,
                                           part_tokens, block_size);
@@ -204,18 +228,31 @@ int32_t nvamd_fp8_decode_attention(void* out, const void* q, const void* k_cache
   p.G = G;
   p.block_size = block_size;
   const int64_t kv_cap = (int64_t)max_num_blocks * block_size;
+  p.mq_max_q = 1;
+  p.scale_log2 = softmax_scale * 1.4426950408889634f;
+  const int ncb = (G + 15) / 16;
+  if (use_stream_k(batch, num_kv_heads, part_tokens)) {
+    const int64_t need = stream_k_bytes(batch, num_kv_heads, G);
+    if (workspace == nullptr || workspace_bytes < need)
+      return fail(NVAMD_ERR_WORKSPACE, "%s: workspace of %lld bytes required (got %lld)", fn,
+                  (long long)need, (long long)workspace_bytes);
+    p.part_tokens = (int)std::min<int64_t>(kv_cap, 0x7fffffff);
+    p.max_parts = 1;
+    p.sk_heads = stream_k_heads(num_kv_heads);
+    p.sk_wgs = stream_k_wgs(ncb, p.sk_heads);
+    p.sk_prefix = static_cast<int32_t*>(workspace);
+    p.sk_part = reinterpret_cast<float*>(static_cast<char*>(workspace) + stream_k_prefix_bytes(batch));
+    return launch_status(nvamd::launch_decode_sk(p, ncb, (hipStream_t)stream), fn);
+  }
   const int64_t part = choose_part_tokens((int64_t)batch * kv_head_groups(num_kv_heads), kv_cap,
                                           part_tokens, block_size);
   p.part_tokens = (int)part;
   p.max_parts = (int)ceil_div(kv_cap, part);
-  p.mq_max_q = 1;
-  p.scale_log2 = softmax_scale * 1.4426950408889634f;
   const int64_t need = partial_bytes(p.q_rows, p.Hq, p.max_parts);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
     return fail(NVAMD_ERR_WORKSPACE, "%s: workspace of %lld bytes required (got %lld)", fn,
                 (long long)need, (long long)workspace_bytes);
   set_partials(p, need > 0 ? workspace : nullptr);
-  const int ncb = (G + 15) / 16;
   return launch_status(nvamd::launch_paged_mq(p, ncb, (hipStream_t)stream), fn);
 }
 

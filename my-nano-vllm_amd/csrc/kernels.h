@@ -27,7 +27,17 @@ struct MqParams {
   int part_tokens, max_parts;
   int mq_max_q;                 // varlen mode: only sequences with 1 <= Lq <= mq_max_q
   float scale_log2;
+  // Balanced decode (stream-K over KV stages), see decode_sk_kernel.
+  float* sk_part;               // [sk_wgs, 2, sk_heads, G, kSkSlotFloats] partial (acc, m, l)
+  int32_t* sk_prefix;           // [num_seqs + 1] stages per kv-head group before each sequence
+  int sk_wgs;                   // persistent workgroups
+  int sk_heads;                 // kv heads per workgroup (4 or 8; one wave each)
 };
+
+// Balanced decode: 16-token stages.
+constexpr int kSkStageTokens = 16;
+constexpr int kSkSlotFloats = 132;  // acc[128], m, l, 2 pad
+constexpr int kSkMaxSeqs = 6136;    // the stage prefix and lengths (2 * num_seqs + 1 ints) fit the 48 KiB LDS ring
 
 // Waves per prefill workgroup: each owns 32 query rows of one head.
 constexpr int kPrefillWaves = 8;
@@ -61,6 +71,9 @@ hipError_t launch_kv_store(const void* key, int64_t key_stride, const void* valu
                            int64_t num_slots, bool vec, hipStream_t stream);
 
 hipError_t launch_paged_mq(const MqParams& p, int ncb, hipStream_t stream);
+// Persistent workgroups the balanced decode kernel keeps resident per CU.
+int decode_sk_wgs_per_cu(int ncb, int hg);
+hipError_t launch_decode_sk(const MqParams& p, int ncb, hipStream_t stream);
 
 // Device bytes of the work list the prefill launch writes (sorted items).
 int64_t prefill_schedule_bytes(const PrefillParams& p);

@@ -37,6 +37,8 @@
 // A sequence that fits in one partition is normalised and written directly;
 // otherwise the partition writes (m, l, acc) and mq_reduce_kernel merges the
 // partitions with the log-sum-exp identity.
+#include <atomic>
+
 #include "fp8_common.h"
 #include "kernels.h"
 
@@ -614,6 +616,416 @@ __global__ __launch_bounds__(256) void mq_reduce_varlen_kernel(MqParams p) {
     if (row >= p.q_rows) break;
     merge_partitions(p, row * p.Hq + idx % p.Hq, Lk, lane);
   }
+}
+
+// ---------------------------------------------------------------------------
+// Balanced decode: stream-K over KV stages
+// ---------------------------------------------------------------------------
+// Pure decode (one query row per sequence) with Hkv % 4 == 0.  A pair =
+// (sequence b, group hg of 4 kv heads); its n_b = ceil(L_b / 16) stages of
+// 16 tokens are laid end to end in (b, hg) order, T stages in all.
+// Workgroup w of a persistent grid of W (as many as stay resident) streams
+// stages [w*T/W, (w+1)*T/W), so every workgroup moves the same KV bytes
+// whatever the context lengths; the uneven per-sequence workgroups of
+// paged_mq_attn_kernel leave the machine half idle at the end of a batch.
+// Wave i owns kv head 4*hg + i and all 16 tokens of each stage (one token
+// row slice of 512 bytes per stage row), so no cross-wave merge is needed.
+// A pair inside one range is finished by its workgroup; a pair cut by range
+// boundaries leaves (acc, m, l) per workgroup in the workspace (slot 0: the
+// range's first pair, slot 1: its last) and decode_sk_merge_kernel combines
+// them.  Loads at a pair boundary (query, context length, block-table
+// window) are ordinary loads whose wait also drains the stage pipeline; a
+// workgroup meets one or two boundaries.
+
+// Workgroup holding stage x of T split over W workgroups.
+__device__ __forceinline__ int sk_owner(int64_t x, int64_t T, int W) {
+  return (int)(((x + 1) * W + T - 1) / T) - 1;
+}
+
+__device__ __forceinline__ int sk_capacity(const MqParams& p) {
+  return (int)min(p.bt_stride * (int64_t)p.block_size, (int64_t)0x7fffffff);
+}
+
+__device__ __forceinline__ int sk_stages(int L) { return L > 0 ? (L + kSkStageTokens - 1) / kSkStageTokens : 0; }
+
+// Stage of the balanced kernel: 16 token rows of HG*128 bytes (K, then V),
+// fetched by 64*HG lanes as 2*HG 1 KiB direct-to-LDS loads per half.
+template <int HG>
+struct SkStage {
+  static constexpr int kTS = kSkStageTokens;
+  static constexpr int kRowBytes = HG * kHeadDim;
+  static constexpr int kHalf = kTS * kRowBytes;      // 8 KiB (HG 4) or 16 KiB (HG 8)
+  static constexpr int kBytes = 2 * kHalf;
+  static constexpr int kRowsPerLoad = 8 / HG;
+  static constexpr int kLanesPerRow = 8 * HG;
+  static constexpr int kRing = kStages * kBytes;
+};
+
+template <int NCB, int HG>
+__global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p) {
+  using S = SkStage<HG>;
+  static_assert(HG == 4 || HG == 8, "4 or 8 kv heads per workgroup");
+  constexpr int kRingBytes = S::kRing;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kRingBytes];
+  const uint32_t lds_smem = wave_uniform((int)lds_addr(smem));
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = wave_uniform(tid >> 6);
+  const int gam = lane >> 4, r = lane & 15;
+  const int G = p.G;
+  const int NHG = p.Hkv / HG;
+  const int B = p.num_seqs;
+  const int W = p.sk_wgs;
+  const int w = blockIdx.x;
+  constexpr int kThreads = 64 * HG;
+  const int cap = sk_capacity(p);
+
+  // ---- stage prefix over the sequences, built in the (still idle) ring -------
+  int* pre = reinterpret_cast<int*>(smem);                 // pre[b] = sum of n_b' for b' < b
+  int* lens = pre + (B + 1);                               // lens[b] = L_b (clamped)
+  int* wtot = pre + (kRingBytes / 4 - 8);                  // per-wave totals of a chunk (HG <= 8)
+  if (tid == 0) pre[0] = 0;
+  int carry = 0;
+  for (int base = 0; base < B; base += kThreads) {
+    const int b = base + tid;
+    const int L = (b < B) ? min(p.context_lens[b], cap) : 0;
+    if (b < B) lens[b] = L;
+    const int n = sk_stages(L);
+    int incl = n;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int o = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += o;
+    }
+    if (lane == 63) wtot[wave] = incl;
+    __syncthreads();
+    int wb = carry;
+    for (int k = 0; k < wave; ++k) wb += wtot[k];
+    if (b < B) pre[b + 1] = wb + incl;
+#pragma unroll
+    for (int k = 0; k < HG; ++k) carry += wtot[k];
+    __syncthreads();
+  }
+  const int64_t T = (int64_t)NHG * carry;
+  if (w == 0)
+    for (int b = tid; b <= B; b += kThreads) p.sk_prefix[b] = pre[b];
+  const int64_t start = (int64_t)w * T / W, end = (int64_t)(w + 1) * T / W;
+  if (start >= end) return;
+  // first pair: the last sequence b0 with NHG * pre[b0] <= start
+  int lo = 0, hi = B - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if ((int64_t)NHG * pre[mid] <= start) lo = mid;
+    else hi = mid - 1;
+  }
+  const int b0 = lo;
+  const int n0 = pre[b0 + 1] - pre[b0];
+  const int64_t rem = start - (int64_t)NHG * pre[b0];
+  const int hg0 = (int)(rem / n0), o0 = (int)(rem - (int64_t)hg0 * n0);
+  const int n_w = (int)(end - start);
+  const int L0 = lens[b0];
+  __syncthreads();  // the prefix is read; the ring is about to be filled
+
+  const int64_t rs = (int64_t)p.Hkv * kHeadDim;  // bytes between token rows
+
+  // ---- fetch side: 1 KiB loads of whole HG*128-byte row slices, swizzled by row
+  uint32_t fetch_off[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int row = (2 * wave + i) * S::kRowsPerLoad + lane / S::kLanesPerRow;
+    const int gran = (lane % S::kLanesPerRow) ^ (row & 7);
+    fetch_off[i] = (uint32_t)row * (uint32_t)rs + 16u * (uint32_t)gran;
+  }
+
+  // Issue cursor: pair (ib, ihg), stage io of in_ in it, sequence length iL,
+  // block-table window (lane l holds entry win + l of sequence ib).
+  int ib = b0, ihg = hg0, io = o0, in_ = n0;
+  int iL = L0;
+  int win = 0, bt_lane = 0;
+  bool win_ok = false;
+  auto load_window_nowait = [&](int bi) {
+    win = bi;
+    const int idx = min(bi + lane, (int)p.bt_stride - 1);
+    bt_lane = p.block_tables[(int64_t)ib * p.bt_stride + idx];
+    win_ok = true;
+  };
+  auto load_window = [&](int bi) {
+    load_window_nowait(bi);
+    consume_i32(bt_lane);
+  };
+  // next pair with stages (only called while stages remain in the range)
+  auto next_pair = [&](int& b, int& hg, int& n, int& L) {
+    if (++hg == NHG) {
+      hg = 0;
+      do {
+        ++b;
+        L = (b < B) ? min(p.context_lens[b], cap) : 0;
+        consume_i32(L);
+        n = sk_stages(L);
+      } while (n == 0 && b < B - 1);
+    }
+  };
+  int issued = 0;
+  auto issue_stage = [&](int slot) {
+    int nvalid = 0;
+    int64_t row = 0;
+    const bool live = issued < n_w;
+    if (live) {
+      const int tok = io * kSkStageTokens;
+      nvalid = min(kSkStageTokens, iL - tok);
+      const int bi = tok / p.block_size;
+      if (!win_ok || bi < win || bi >= win + 64) load_window(bi);
+      const int blk = __builtin_amdgcn_readlane(bt_lane, bi - win);
+      row = (int64_t)blk * p.block_size + (tok - bi * p.block_size);
+      if (blk < 0 || row + kSkStageTokens > p.kv_rows) nvalid = 0;
+    }
+    if (nvalid <= 0) {
+      nvalid = 0;
+      row = 0;
+    }
+    const int64_t base = (row * p.Hkv + ihg * HG) * kHeadDim;
+    const uint32_t nbytes = (uint32_t)(nvalid * rs);
+    const u32x4 rk = rsrc_words(p.k + base, nbytes);
+    const u32x4 rv = rsrc_words(p.v + base, nbytes);
+    const uint32_t dst = lds_smem + (uint32_t)(slot * S::kBytes + (2 * wave) * 1024);
+    dma_load16(rk, fetch_off[0], dst);
+    dma_load16(rk, fetch_off[1], dst + 1024u);
+    dma_load16(rv, fetch_off[0], dst + (uint32_t)S::kHalf);
+    dma_load16(rv, fetch_off[1], dst + (uint32_t)S::kHalf + 1024u);
+    if (live) {
+      ++issued;
+      if (++io == in_ && issued < n_w) {
+        const int prev_b = ib;
+        next_pair(ib, ihg, in_, iL);
+        io = 0;
+        if (ib != prev_b) win_ok = false;
+      }
+    }
+  };
+
+  // ---- read side: head `wave`, token row r of the stage ------------------------
+  uint32_t k_rd[2], v_rd[4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+    k_rd[i] = (uint32_t)(r * S::kRowBytes + 16 * ((8 * wave + 4 * i + gam) ^ (r & 7)));
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int rv = 4 * gam + e;
+    v_rd[e] = (uint32_t)(S::kHalf + rv * S::kRowBytes + 16 * ((8 * wave + (r >> 1)) ^ (rv & 7)) + 8 * (r & 1));
+  }
+
+  // ---- compute cursor: pair (cb_s, chg), stage co of cn, length cL -------------
+  int cb_s = b0, chg = hg0, co = o0, cn = n0;
+  int cL = L0;
+  bool first_seg = true;
+  int seg_o0 = o0;
+  bf16x8 qop[NCB][4];
+  int col_limit[NCB];
+  float m[NCB], lsum[NCB];
+  f32x4 acc[NCB][8];
+  auto begin_pair = [&]() {
+    const int kvh = chg * HG + wave;
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) {
+      const int col = 16 * cb + r;
+      const bool valid = col < G;
+      col_limit[cb] = valid ? cL : 0;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        u32x4 a = {0u, 0u, 0u, 0u}, b = {0u, 0u, 0u, 0u};
+        if (valid) {
+          const uint16_t* qp = p.q + ((int64_t)cb_s * p.Hq + kvh * G + col) * kHeadDim + 16 * gam + 64 * h;
+          a = *reinterpret_cast<const u32x4*>(qp);
+          b = *reinterpret_cast<const u32x4*>(qp + 8);
+        }
+        qop[cb][2 * h + 0] = as_bf16x8(a);
+        qop[cb][2 * h + 1] = as_bf16x8(b);
+      }
+      m[cb] = -INFINITY;
+      lsum[cb] = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[cb][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) consume(qop[cb][c]);
+  };
+  // Writes the output of a pair finished here, or the partial of a cut pair.
+  auto end_segment = [&](bool full) {
+    const int kvh = chg * HG + wave;
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) {
+      lsum[cb] += shfl_xor_f32(lsum[cb], 16);
+      lsum[cb] += shfl_xor_f32(lsum[cb], 32);
+      const int col = 16 * cb + r;
+      if (col >= G) continue;
+      if (full) {
+        const float inv = (lsum[cb] > 0.f) ? 1.0f / lsum[cb] : 0.f;
+        uint16_t* op = p.out + ((int64_t)cb_s * p.Hq + kvh * G + col) * kHeadDim + 32 * gam;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          float o[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[i] = acc[cb][i][k];
+          store_out_row8(op + 8 * k, o, inv);
+        }
+      } else {
+        const int slot = first_seg ? 0 : 1;
+        float* ps = p.sk_part + ((((int64_t)w * 2 + slot) * HG + wave) * G + col) * kSkSlotFloats;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          *reinterpret_cast<f32x4*>(ps + 32 * gam + 8 * k) =
+              f32x4{acc[cb][0][k], acc[cb][1][k], acc[cb][2][k], acc[cb][3][k]};
+          *reinterpret_cast<f32x4*>(ps + 32 * gam + 8 * k + 4) =
+              f32x4{acc[cb][4][k], acc[cb][5][k], acc[cb][6][k], acc[cb][7][k]};
+        }
+        if (gam == 0) {
+          ps[kHeadDim] = m[cb];
+          ps[kHeadDim + 1] = lsum[cb];
+        }
+      }
+    }
+  };
+
+  // the first pair's block-table window and query load together
+  load_window_nowait(o0 * kSkStageTokens / p.block_size);
+  begin_pair();
+  consume_i32(bt_lane);
+  issue_stage(0);
+  issue_stage(1);
+  for (int s = 0; s < n_w; ++s) {
+    wait_vmcnt<4>();   // this wave's loads of stage s have landed (stage s+1's 4 may not)
+    lds_barrier();     // ... and every wave's; slot (s+2)%3 is no longer being read
+    issue_stage((s + 2) % kStages);
+    const uint8_t* sl = smem + (s % kStages) * S::kBytes;
+    ChunkRegs cr;
+    cr.k[0] = lds_read16(sl + k_rd[0]);
+    cr.k[1] = lds_read16(sl + k_rd[1]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) cr.v[e] = lds_read8(sl + v_rd[e]);
+    const int tok0 = co * kSkStageTokens;
+    attend_chunk<NCB>(cr, qop, col_limit, tok0, tok0 + kSkStageTokens > cL, p.scale_log2, gam, m, lsum, acc);
+    if (++co == cn || s == n_w - 1) {
+      end_segment(seg_o0 == 0 && co == cn);
+      if (s < n_w - 1) {
+        next_pair(cb_s, chg, cn, cL);
+        co = 0;
+        seg_o0 = 0;
+        first_seg = false;
+        begin_pair();
+      }
+    }
+  }
+  wait_vmcnt<0>();  // nothing may land in LDS after the workgroup exits
+}
+
+// Merges the partials of one pair cut across workgroups (or zero-fills a
+// row with an empty context).  One wave per (sequence, query head): lane i
+// reads (m, l) of the i-th contributing workgroup, the wave reduces them,
+// then every lane accumulates 2 dims over the contributions.
+__global__ __launch_bounds__(256) void decode_sk_merge_kernel(MqParams p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (gw >= (int64_t)p.num_seqs * p.Hq) return;
+  const int b = (int)(gw / p.Hq), hq = (int)(gw - (int64_t)b * p.Hq);
+  const int G = p.G, HG = p.sk_heads, NHG = p.Hkv / HG;
+  const int kvh = hq / G, col = hq - kvh * G;
+  const int hg = kvh / HG, hh = kvh - hg * HG;
+  const int L = min(p.context_lens[b], sk_capacity(p));
+  const int n = sk_stages(L);
+  uint32_t* out = reinterpret_cast<uint32_t*>(p.out + gw * kHeadDim);
+  if (n == 0) {
+    // Empty context (graph padding rows): the reference yields NaN here; write 0.
+    out[lane] = 0u;
+    return;
+  }
+  const int W = p.sk_wgs;
+  const int64_t T = (int64_t)NHG * p.sk_prefix[p.num_seqs];
+  const int64_t P = (int64_t)NHG * p.sk_prefix[b] + (int64_t)hg * n;
+  const int wf = sk_owner(P, T, W), wl = sk_owner(P + n - 1, T, W);
+  if (wf == wl) return;  // finished by its workgroup
+  // Workgroups in (wf, wl] start inside the pair; those with empty ranges
+  // (more workgroups than stages) wrote nothing and are skipped.
+  auto slot_ptr = [&](int w) -> const float* {
+    const int64_t s0 = (int64_t)w * T / W;
+    if (s0 == (int64_t)(w + 1) * T / W) return nullptr;
+    const int slot = (s0 < P) ? 1 : 0;
+    return p.sk_part + ((((int64_t)w * 2 + slot) * HG + hh) * G + col) * kSkSlotFloats;
+  };
+  float M = -INFINITY, Lsum = 0.f, o0 = 0.f, o1 = 0.f;
+  for (int w0 = wf; w0 <= wl; w0 += 64) {
+    const int cnt = min(64, wl - w0 + 1);
+    float mi = -INFINITY, li = 0.f;
+    if (lane < cnt) {
+      if (const float* ps = slot_ptr(w0 + lane)) {
+        mi = ps[kHeadDim];
+        li = ps[kHeadDim + 1];
+      }
+    }
+    float Mp = mi;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) Mp = fmaxf(Mp, shfl_xor_f32(Mp, off));
+    const float Mn = fmaxf(M, Mp);
+    const float Ms = (Mn == -INFINITY) ? 0.f : Mn;
+    const float sc = (M == -INFINITY) ? 0.f : fast_exp2(M - Ms);
+    Lsum *= sc;
+    o0 *= sc;
+    o1 *= sc;
+    M = Mn;
+    const float wi = (mi == -INFINITY) ? 0.f : fast_exp2(mi - Ms);
+    float lw = li * wi;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) lw += shfl_xor_f32(lw, off);
+    Lsum += lw;
+    for (int k = 0; k < cnt; ++k) {
+      const float wk = __shfl(wi, k, 64);
+      if (wk == 0.f) continue;
+      const f32x2 a = *reinterpret_cast<const f32x2*>(slot_ptr(w0 + k) + 2 * lane);
+      o0 += wk * a.x;
+      o1 += wk * a.y;
+    }
+  }
+  const float inv = (Lsum > 0.f) ? 1.0f / Lsum : 0.f;
+  out[lane] = out_round_bf16_bits(o0 * inv) | (out_round_bf16_bits(o1 * inv) << 16);
+}
+
+namespace {
+template <int NCB, int HG>
+int sk_occupancy() {
+  static std::atomic<int> cached{0};  // the kernel's occupancy does not change
+  int n = cached.load(std::memory_order_relaxed);
+  if (n > 0) return n;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_sk_kernel<NCB, HG>, 64 * HG, 0) != hipSuccess || n <= 0)
+    return 1;  // no device: not cached
+  cached.store(n, std::memory_order_relaxed);
+  return n;
+}
+}  // namespace
+
+int decode_sk_wgs_per_cu(int ncb, int hg) {
+  if (hg == 8) return ncb == 1 ? sk_occupancy<1, 8>() : sk_occupancy<2, 8>();
+  return ncb == 1 ? sk_occupancy<1, 4>() : sk_occupancy<2, 4>();
+}
+
+hipError_t launch_decode_sk(const MqParams& p, int ncb, hipStream_t stream) {
+  if (p.num_seqs == 0) return hipSuccess;
+  const int hg = p.sk_heads;
+  if ((hg != 4 && hg != 8) || p.Hkv % hg != 0 || p.num_seqs > kSkMaxSeqs || p.sk_wgs <= 0 || p.cu_q != nullptr ||
+      (ncb != 1 && ncb != 2))
+    return hipErrorInvalidValue;
+  const dim3 grid((unsigned)p.sk_wgs), block((unsigned)(64 * hg));
+  if (hg == 4) {
+    if (ncb == 1) hipLaunchKernelGGL((decode_sk_kernel<1, 4>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((decode_sk_kernel<2, 4>), grid, block, 0, stream, p);
+  } else {
+    if (ncb == 1) hipLaunchKernelGGL((decode_sk_kernel<1, 8>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((decode_sk_kernel<2, 8>), grid, block, 0, stream, p);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t waves = (int64_t)p.num_seqs * p.Hq;
+  hipLaunchKernelGGL(decode_sk_merge_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream, p);
+  return hipGetLastError();
 }
 
 hipError_t launch_paged_mq(const MqParams& p, int ncb, hipStream_t stream) {
