@@ -97,14 +97,14 @@ bool use_stream_k(int32_t batch, int32_t num_kv_heads, int32_t part_tokens) {
 // kv heads come in 8s (each workgroup then reads whole DRAM pages), else 4.
 int stream_k_heads(int32_t num_kv_heads) { return num_kv_heads % 8 == 0 ? 8 : 4; }
 
-int stream_k_wgs(int ncb, int hg) { return device_cu_count() * nvamd::decode_sk_wgs_per_cu(ncb, hg); }
+int stream_k_wgs(int ncb, int hg, int G) { return device_cu_count() * nvamd::decode_sk_wgs_per_cu(ncb, hg, G); }
 
 // Workspace of the balanced decode: the stage prefix, then the partial slots.
 int64_t stream_k_prefix_bytes(int32_t batch) { return (((int64_t)batch + 1) * 4 + 255) / 256 * 256; }
 int64_t stream_k_bytes(int32_t batch, int32_t num_kv_heads, int32_t G) {
   const int ncb = (G + 15) / 16, hg = stream_k_heads(num_kv_heads);
   return stream_k_prefix_bytes(batch) +
-         (int64_t)stream_k_wgs(ncb, hg) * 2 * hg * G * nvamd::kSkSlotFloats * (int64_t)sizeof(float);
+         (int64_t)stream_k_wgs(ncb, hg, G) * 2 * hg * G * nvamd::kSkSlotFloats * (int64_t)sizeof(float);
 }
 
 void set_partials(nvamd::MqParams& p, void* workspace) {
@@ -239,7 +239,7 @@ int32_t nvamd_fp8_decode_attention(void* out, const void* q, const void* k_cache
     p.part_tokens = (int)std::min<int64_t>(kv_cap, 0x7fffffff);
     p.max_parts = 1;
     p.sk_heads = stream_k_heads(num_kv_heads);
-    p.sk_wgs = stream_k_wgs(ncb, p.sk_heads);
+    p.sk_wgs = stream_k_wgs(ncb, p.sk_heads, G);
     p.sk_prefix = static_cast<int32_t*>(workspace);
     p.sk_part = reinterpret_cast<float*>(static_cast<char*>(workspace) + stream_k_prefix_bytes(batch));
     return launch_status(nvamd::launch_decode_sk(p, ncb, (hipStream_t)stream), fn);

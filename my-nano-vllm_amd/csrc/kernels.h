@@ -72,7 +72,7 @@ hipError_t launch_kv_store(const void* key, int64_t key_stride, const void* valu
 
 hipError_t launch_paged_mq(const MqParams& p, int ncb, hipStream_t stream);
 // Persistent workgroups the balanced decode kernel keeps resident per CU.
-int decode_sk_wgs_per_cu(int ncb, int hg);
+int decode_sk_wgs_per_cu(int ncb, int hg, int G);
 hipError_t launch_decode_sk(const MqParams& p, int ncb, hipStream_t stream);
 
 // Device bytes of the work list the prefill launch writes (sorted items).

@@ -637,6 +637,12 @@ __global__ __launch_bounds__(256) void mq_reduce_varlen_kernel(MqParams p) {
 // window) are ordinary loads whose wait also drains the stage pipeline; a
 // workgroup meets one or two boundaries.
 
+// Wave-uniform read through the scalar data cache (constant address space:
+// the tables are not written while the kernel runs).
+__device__ __forceinline__ int sload_i32(const int32_t* base, int64_t i) {
+  return ((const __attribute__((address_space(4))) int32_t*)base)[i];
+}
+
 // Workgroup holding stage x of T split over W workgroups.
 __device__ __forceinline__ int sk_owner(int64_t x, int64_t T, int W) {
   return (int)(((x + 1) * W + T - 1) / T) - 1;
@@ -649,22 +655,28 @@ __device__ __forceinline__ int sk_capacity(const MqParams& p) {
 __device__ __forceinline__ int sk_stages(int L) { return L > 0 ? (L + kSkStageTokens - 1) / kSkStageTokens : 0; }
 
 // Stage of the balanced kernel: 16 token rows of HG*128 bytes (K, then V),
-// fetched by 64*HG lanes as 2*HG 1 KiB direct-to-LDS loads per half.
-template <int HG>
+// fetched by 64*HG lanes as 2*HG 1 KiB direct-to-LDS loads per half.  With
+// QL the slot also has room for the queries of the HG kv heads (G <=
+// kSkQMaxG), loaded with the first stage of each pair.
+constexpr int kSkQMaxG = 8;
+template <int HG, bool QL>
 struct SkStage {
   static constexpr int kTS = kSkStageTokens;
   static constexpr int kRowBytes = HG * kHeadDim;
   static constexpr int kHalf = kTS * kRowBytes;      // 8 KiB (HG 4) or 16 KiB (HG 8)
   static constexpr int kBytes = 2 * kHalf;
+  static constexpr int kQBytes = QL ? HG * kSkQMaxG * kHeadDim * 2 : 0;
+  static constexpr int kSlot = kBytes + kQBytes;
   static constexpr int kRowsPerLoad = 8 / HG;
   static constexpr int kLanesPerRow = 8 * HG;
-  static constexpr int kRing = kStages * kBytes;
+  static constexpr int kRing = kStages * kSlot;
 };
 
-template <int NCB, int HG>
+template <int NCB, int HG, bool QL>
 __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p) {
-  using S = SkStage<HG>;
+  using S = SkStage<HG, QL>;
   static_assert(HG == 4 || HG == 8, "4 or 8 kv heads per workgroup");
+  static_assert(!QL || NCB == 1, "queries through LDS for G <= 8 only");
   constexpr int kRingBytes = S::kRing;
   __shared__ __attribute__((aligned(16))) uint8_t smem[kRingBytes];
   const uint32_t lds_smem = wave_uniform((int)lds_addr(smem));
@@ -736,21 +748,21 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p) {
     fetch_off[i] = (uint32_t)row * (uint32_t)rs + 16u * (uint32_t)gran;
   }
 
-  // Issue cursor: pair (ib, ihg), stage io of in_ in it, sequence length iL,
-  // block-table window (lane l holds entry win + l of sequence ib).
+  // Issue cursor: pair (ib, ihg), stage io of in_ in it, sequence length
+  // iL; block ibi of the sequence holds the stage at row offset ioff, and
+  // blk_cur / blk_nxt are the table entries of blocks ibi and ibi + 1 (the
+  // next one is read a block ahead).  Table entries and context lengths are
+  // scalar loads, so they never wait for the stage loads in flight.
   int ib = b0, ihg = hg0, io = o0, in_ = n0;
   int iL = L0;
-  int win = 0, bt_lane = 0;
-  bool win_ok = false;
-  auto load_window_nowait = [&](int bi) {
-    win = bi;
-    const int idx = min(bi + lane, (int)p.bt_stride - 1);
-    bt_lane = p.block_tables[(int64_t)ib * p.bt_stride + idx];
-    win_ok = true;
-  };
-  auto load_window = [&](int bi) {
-    load_window_nowait(bi);
-    consume_i32(bt_lane);
+  int ibi = 0, ioff = 0, blk_cur = 0, blk_nxt = 0;
+  auto seek_block = [&]() {  // block entries for stage io of sequence ib
+    const int tok = io * kSkStageTokens;
+    ibi = tok / p.block_size;
+    ioff = tok - ibi * p.block_size;
+    const int64_t row0 = (int64_t)ib * p.bt_stride;
+    blk_cur = sload_i32(p.block_tables, row0 + ibi);
+    blk_nxt = sload_i32(p.block_tables, row0 + min(ibi + 1, (int)p.bt_stride - 1));
   };
   // next pair with stages (only called while stages remain in the range)
   auto next_pair = [&](int& b, int& hg, int& n, int& L) {
@@ -758,25 +770,31 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p) {
       hg = 0;
       do {
         ++b;
-        L = (b < B) ? min(p.context_lens[b], cap) : 0;
-        consume_i32(L);
+        L = (b < B) ? min(sload_i32(p.context_lens, b), cap) : 0;
         n = sk_stages(L);
       } while (n == 0 && b < B - 1);
     }
   };
   int issued = 0;
+  bool q_due = true;  // the next stage issued is the first of a pair in this range
   auto issue_stage = [&](int slot) {
     int nvalid = 0;
     int64_t row = 0;
     const bool live = issued < n_w;
     if (live) {
-      const int tok = io * kSkStageTokens;
-      nvalid = min(kSkStageTokens, iL - tok);
-      const int bi = tok / p.block_size;
-      if (!win_ok || bi < win || bi >= win + 64) load_window(bi);
-      const int blk = __builtin_amdgcn_readlane(bt_lane, bi - win);
-      row = (int64_t)blk * p.block_size + (tok - bi * p.block_size);
-      if (blk < 0 || row + kSkStageTokens > p.kv_rows) nvalid = 0;
+      nvalid = min(kSkStageTokens, iL - io * kSkStageTokens);
+      row = (int64_t)blk_cur * p.block_size + ioff;
+      if (blk_cur < 0 || row + kSkStageTokens > p.kv_rows) nvalid = 0;
+      if (QL && q_due) {
+        // the pair's queries (HG*G rows of 256 bytes, contiguous) into the
+        // slot's query area, before the stage: its wait covers them
+        const int n_q = HG * G * kHeadDim * 2 / 1024;  // 1 KiB loads (2G)
+        const u32x4 rq = rsrc_words(p.q + ((int64_t)ib * p.Hq + (int64_t)ihg * HG * G) * kHeadDim,
+                                    (uint32_t)(n_q * 1024));
+        const uint32_t qdst = lds_smem + (uint32_t)(slot * S::kSlot + S::kBytes);
+        for (int j = wave; j < n_q; j += HG) dma_load16(rq, 1024u * j + 16u * lane, qdst + 1024u * j);
+      }
+      q_due = false;
     }
     if (nvalid <= 0) {
       nvalid = 0;
@@ -786,18 +804,25 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p) {
     const uint32_t nbytes = (uint32_t)(nvalid * rs);
     const u32x4 rk = rsrc_words(p.k + base, nbytes);
     const u32x4 rv = rsrc_words(p.v + base, nbytes);
-    const uint32_t dst = lds_smem + (uint32_t)(slot * S::kBytes + (2 * wave) * 1024);
+    const uint32_t dst = lds_smem + (uint32_t)(slot * S::kSlot + (2 * wave) * 1024);
     dma_load16(rk, fetch_off[0], dst);
     dma_load16(rk, fetch_off[1], dst + 1024u);
     dma_load16(rv, fetch_off[0], dst + (uint32_t)S::kHalf);
     dma_load16(rv, fetch_off[1], dst + (uint32_t)S::kHalf + 1024u);
     if (live) {
       ++issued;
-      if (++io == in_ && issued < n_w) {
-        const int prev_b = ib;
-        next_pair(ib, ihg, in_, iL);
-        io = 0;
-        if (ib != prev_b) win_ok = false;
+      if (++io == in_) {
+        if (issued < n_w) {
+          next_pair(ib, ihg, in_, iL);
+          io = 0;
+          seek_block();
+          q_due = true;
+        }
+      } else if ((ioff += kSkStageTokens) == p.block_size) {
+        ioff = 0;
+        ++ibi;
+        blk_cur = blk_nxt;
+        blk_nxt = sload_i32(p.block_tables, (int64_t)ib * p.bt_stride + min(ibi + 1, (int)p.bt_stride - 1));
       }
     }
   };
@@ -822,6 +847,10 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p) {
   int col_limit[NCB];
   float m[NCB], lsum[NCB];
   f32x4 acc[NCB][8];
+  // New pair: reset the softmax state; the queries are read here from
+  // global memory (!QL: the wait drains the stages in flight) or, with QL,
+  // from the query area of the pair's first stage once it has landed.
+  bool q_from_lds = false;
   auto begin_pair = [&]() {
     const int kvh = chg * HG + wave;
 #pragma unroll
@@ -829,26 +858,45 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p) {
       const int col = 16 * cb + r;
       const bool valid = col < G;
       col_limit[cb] = valid ? cL : 0;
+      if (!QL) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        u32x4 a = {0u, 0u, 0u, 0u}, b = {0u, 0u, 0u, 0u};
-        if (valid) {
-          const uint16_t* qp = p.q + ((int64_t)cb_s * p.Hq + kvh * G + col) * kHeadDim + 16 * gam + 64 * h;
-          a = *reinterpret_cast<const u32x4*>(qp);
-          b = *reinterpret_cast<const u32x4*>(qp + 8);
+        for (int h = 0; h < 2; ++h) {
+          u32x4 a = {0u, 0u, 0u, 0u}, b = {0u, 0u, 0u, 0u};
+          if (valid) {
+            const uint16_t* qp = p.q + ((int64_t)cb_s * p.Hq + kvh * G + col) * kHeadDim + 16 * gam + 64 * h;
+            a = *reinterpret_cast<const u32x4*>(qp);
+            b = *reinterpret_cast<const u32x4*>(qp + 8);
+          }
+          qop[cb][2 * h + 0] = as_bf16x8(a);
+          qop[cb][2 * h + 1] = as_bf16x8(b);
         }
-        qop[cb][2 * h + 0] = as_bf16x8(a);
-        qop[cb][2 * h + 1] = as_bf16x8(b);
       }
       m[cb] = -INFINITY;
       lsum[cb] = 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) acc[cb][i] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
+    if (!QL) {
 #pragma unroll
-    for (int cb = 0; cb < NCB; ++cb)
+      for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) consume(qop[cb][c]);
+        for (int c = 0; c < 4; ++c) consume(qop[cb][c]);
+    }
+    q_from_lds = QL;
+  };
+  // QL: query row (wave * G + col) of the slot's query area, dims 16gam + 64h + 8j.
+  auto read_q = [&](const uint8_t* slot_base) {
+    const uint8_t* qa = slot_base + S::kBytes;
+    const int col = r;  // NCB == 1
+    const bool valid = col < G;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        u32x4 a = {0u, 0u, 0u, 0u};
+        if (valid) a = lds_read16(qa + (wave * G + col) * (kHeadDim * 2) + (16 * gam + 64 * h + 8 * j) * 2);
+        qop[0][2 * h + j] = as_bf16x8(a);
+      }
   };
   // Writes the output of a pair finished here, or the partial of a cut pair.
   auto end_segment = [&](bool full) {
@@ -887,17 +935,19 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p) {
     }
   };
 
-  // the first pair's block-table window and query load together
-  load_window_nowait(o0 * kSkStageTokens / p.block_size);
+  seek_block();
   begin_pair();
-  consume_i32(bt_lane);
   issue_stage(0);
   issue_stage(1);
   for (int s = 0; s < n_w; ++s) {
     wait_vmcnt<4>();   // this wave's loads of stage s have landed (stage s+1's 4 may not)
     lds_barrier();     // ... and every wave's; slot (s+2)%3 is no longer being read
     issue_stage((s + 2) % kStages);
-    const uint8_t* sl = smem + (s % kStages) * S::kBytes;
+    const uint8_t* sl = smem + (s % kStages) * S::kSlot;
+    if (QL && q_from_lds) {
+      read_q(sl);
+      q_from_lds = false;
+    }
     ChunkRegs cr;
     cr.k[0] = lds_read16(sl + k_rd[0]);
     cr.k[1] = lds_read16(sl + k_rd[1]);
@@ -990,21 +1040,34 @@ __global__ __launch_bounds__(256) void decode_sk_merge_kernel(MqParams p) {
 }
 
 namespace {
-template <int NCB, int HG>
+template <int NCB, int HG, bool QL>
 int sk_occupancy() {
   static std::atomic<int> cached{0};  // the kernel's occupancy does not change
   int n = cached.load(std::memory_order_relaxed);
   if (n > 0) return n;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_sk_kernel<NCB, HG>, 64 * HG, 0) != hipSuccess || n <= 0)
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_sk_kernel<NCB, HG, QL>, 64 * HG, 0) != hipSuccess ||
+      n <= 0)
     return 1;  // no device: not cached
   cached.store(n, std::memory_order_relaxed);
   return n;
 }
+
+// Instantiation: 0 = <1,4,-> 1 = <2,4,-> 2 = <1,8,QL> 3 = <1,8,-> 4 = <2,8,->
+int sk_variant(int ncb, int hg, int G) {
+  if (hg == 4) return ncb == 1 ? 0 : 1;
+  if (ncb == 2) return 4;
+  return G <= kSkQMaxG ? 2 : 3;
+}
 }  // namespace
 
-int decode_sk_wgs_per_cu(int ncb, int hg) {
-  if (hg == 8) return ncb == 1 ? sk_occupancy<1, 8>() : sk_occupancy<2, 8>();
-  return ncb == 1 ? sk_occupancy<1, 4>() : sk_occupancy<2, 4>();
+int decode_sk_wgs_per_cu(int ncb, int hg, int G) {
+  switch (sk_variant(ncb, hg, G)) {
+    case 0: return sk_occupancy<1, 4, false>();
+    case 1: return sk_occupancy<2, 4, false>();
+    case 2: return sk_occupancy<1, 8, true>();
+    case 3: return sk_occupancy<1, 8, false>();
+    default: return sk_occupancy<2, 8, false>();
+  }
 }
 
 hipError_t launch_decode_sk(const MqParams& p, int ncb, hipStream_t stream) {
@@ -1014,12 +1077,12 @@ hipError_t launch_decode_sk(const MqParams& p, int ncb, hipStream_t stream) {
       (ncb != 1 && ncb != 2))
     return hipErrorInvalidValue;
   const dim3 grid((unsigned)p.sk_wgs), block((unsigned)(64 * hg));
-  if (hg == 4) {
-    if (ncb == 1) hipLaunchKernelGGL((decode_sk_kernel<1, 4>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((decode_sk_kernel<2, 4>), grid, block, 0, stream, p);
-  } else {
-    if (ncb == 1) hipLaunchKernelGGL((decode_sk_kernel<1, 8>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((decode_sk_kernel<2, 8>), grid, block, 0, stream, p);
+  switch (sk_variant(ncb, hg, p.G)) {
+    case 0: hipLaunchKernelGGL((decode_sk_kernel<1, 4, false>), grid, block, 0, stream, p); break;
+    case 1: hipLaunchKernelGGL((decode_sk_kernel<2, 4, false>), grid, block, 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((decode_sk_kernel<1, 8, true>), grid, block, 0, stream, p); break;
+    case 3: hipLaunchKernelGGL((decode_sk_kernel<1, 8, false>), grid, block, 0, stream, p); break;
+    default: hipLaunchKernelGGL((decode_sk_kernel<2, 8, false>), grid, block, 0, stream, p); break;
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
