@@ -1002,19 +1002,30 @@ __global__ __launch_bounds__(256) void decode_sk_merge_kernel(MqParams p) {
     const int slot = (s0 < P) ? 1 : 0;
     return p.sk_part + ((((int64_t)w * 2 + slot) * HG + hh) * G + col) * kSkSlotFloats;
   };
+  // Contributors in chunks of 8: all of a chunk's loads (lane j < 8 reads
+  // (m, l) of contributor j, every lane its 2 dims of each) are issued
+  // before any is used, so a chunk costs one memory round trip.
   float M = -INFINITY, Lsum = 0.f, o0 = 0.f, o1 = 0.f;
-  for (int w0 = wf; w0 <= wl; w0 += 64) {
-    const int cnt = min(64, wl - w0 + 1);
+  for (int w0 = wf; w0 <= wl; w0 += 8) {
+    const int cnt = min(8, wl - w0 + 1);
     float mi = -INFINITY, li = 0.f;
-    if (lane < cnt) {
-      if (const float* ps = slot_ptr(w0 + lane)) {
-        mi = ps[kHeadDim];
-        li = ps[kHeadDim + 1];
+    f32x2 a[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      a[j] = f32x2{0.f, 0.f};
+      const float* ps = (j < cnt) ? slot_ptr(w0 + j) : nullptr;
+      if (ps != nullptr) {
+        a[j] = *reinterpret_cast<const f32x2*>(ps + 2 * lane);
+        if (lane == j) {
+          mi = ps[kHeadDim];
+          li = ps[kHeadDim + 1];
+        }
       }
     }
     float Mp = mi;
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) Mp = fmaxf(Mp, shfl_xor_f32(Mp, off));
+    for (int off = 4; off > 0; off >>= 1) Mp = fmaxf(Mp, shfl_xor_f32(Mp, off));
+    Mp = __shfl(Mp, 0, 64);  // lanes 0..7 hold the chunk's values
     const float Mn = fmaxf(M, Mp);
     const float Ms = (Mn == -INFINITY) ? 0.f : Mn;
     const float sc = (M == -INFINITY) ? 0.f : fast_exp2(M - Ms);
@@ -1025,14 +1036,13 @@ __global__ __launch_bounds__(256) void decode_sk_merge_kernel(MqParams p) {
     const float wi = (mi == -INFINITY) ? 0.f : fast_exp2(mi - Ms);
     float lw = li * wi;
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) lw += shfl_xor_f32(lw, off);
-    Lsum += lw;
-    for (int k = 0; k < cnt; ++k) {
-      const float wk = __shfl(wi, k, 64);
-      if (wk == 0.f) continue;
-      const f32x2 a = *reinterpret_cast<const f32x2*>(slot_ptr(w0 + k) + 2 * lane);
-      o0 += wk * a.x;
-      o1 += wk * a.y;
+    for (int off = 4; off > 0; off >>= 1) lw += shfl_xor_f32(lw, off);
+    Lsum += __shfl(lw, 0, 64);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float wk = __shfl(wi, j, 64);
+      o0 += wk * a[j].x;
+      o1 += wk * a[j].y;
     }
   }
   const float inv = (Lsum > 0.f) ? 1.0f / Lsum : 0.f;

@@ -132,3 +132,29 @@ def test_balanced_decode_workspace_is_required():
                                         bt.shape[1], SCALE, 0, ws.data_ptr(), need - 1,
                                         torch.cuda.current_stream().cuda_stream)
     assert st != 0 and b"workspace" in lib.nvamd_last_error()
+
+
+def test_balanced_decode_garbage_and_reused_workspace():
+    """The workspace needs no initialisation: random bytes in it (including
+    the arrival words of cut pairs) and reuse across calls give the same
+    result as the oracle."""
+    wl = W.decode_workload("bal_ws_garbage", 96, 16, 8, 1, 3000, seed=12)
+    announce("balanced decode: garbage / reused workspace")
+    cpu_c, gpu_c = build_pair(wl)
+    q = wl.make_q("cpu")
+    qg = q.cuda()
+    bt = torch.from_numpy(wl.block_tables).cuda()
+    ctx = torch.from_numpy(wl.context_lens()).cuda()
+    lib = _native.load()
+    nb = bt.shape[1]
+    need = lib.nvamd_decode_workspace_bytes(96, 16, 8, nb, 256, 0)
+    ws = torch.randint(0, 256, (need,), dtype=torch.uint8, device="cuda")
+    want = _oracle(wl, cpu_c, q)
+    for call in range(3):
+        out = torch.empty_like(qg)
+        st = lib.nvamd_fp8_decode_attention(out.data_ptr(), qg.data_ptr(), gpu_c[0].data_ptr(), gpu_c[1].data_ptr(),
+                                            bt.data_ptr(), ctx.data_ptr(), 96, 16, 8, 128, wl.num_blocks, 256, nb,
+                                            SCALE, 0, ws.data_ptr(), need, torch.cuda.current_stream().cuda_stream)
+        _native.check(st, "decode")
+        torch.cuda.synchronize()
+        assert_close(out, want, f"garbage_ws call {call}")
