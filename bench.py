@@ -4,15 +4,18 @@ Headline (``value``): FP8 paged decode at Qwen3-0.6B attention shapes (16
 query / 8 kv heads, head_dim 128, block 256, B = 256 sequences, context
 U[100, 2048], seeded), as achieved HBM GB/s over the algorithmic bytes of a
 step: each FP8 K/V byte once + bf16 Q in and O out + the block-table row and
-context length of every sequence.  At this shape one decode call is one
-kernel launch (``paged_mq_attn_kernel``; the split-KV reduce is not needed),
-so the HIP-event time of a call is that kernel's duration.
+context length of every sequence.  One decode call is two launches: the
+balanced stream-K pass (``decode_sk_kernel<1,8,QL>``, one persistent
+workgroup per CU streaming an equal share of the KV stages) and the merge
+pass for sequences cut between workgroups (``decode_sk_merge_kernel``).  The
+HIP-event time of a call covers both, so ``roofline.achieved`` is the
+algorithmic bytes over the two launches together.
 
 Secondary fields in the same JSON line:
   prefill      varlen chunked prefill at Qwen3-8B shapes (32/8 heads, 16 x
                512-token chunks over cached context U[0, 4096]) in TFLOP/s of
                unmasked causal pairs, vs the bf16 dense MFMA peak;
-  long_decode  split-KV decode at Qwen3-32B shapes (64/8 heads, B = 32,
+  long_decode  long-context decode at Qwen3-32B shapes (64/8 heads, B = 32,
                context U[32K, 128K], 1% of K/V x20).
 
 Inputs are resident in HBM before timing; two KV pools with different
@@ -217,7 +220,7 @@ def main():
                     ms_per_step=round(res["ms"], 5),
                     roofline=dict(bound="hbm", achieved=round(res["gbs"], 2), peak=HBM_PEAK_GBS,
                                   unit="GB/s", frac=round(res["gbs"] / HBM_PEAK_GBS, 4),
-                                  traffic=_traffic_from_profile(), kernel="paged_mq_attn_kernel<1,2>",
+                                  traffic=_traffic_from_profile(), kernel="decode_sk_kernel<1,8,QL> + decode_sk_merge_kernel",
                                   algorithmic_bytes_per_launch=res["bytes"]),
                     config=dict(workload=wl.name, batch=wl.num_seqs, num_heads=wl.num_heads,
                                 num_kv_heads=wl.num_kv_heads, head_dim=128, block_size=wl.block_size,
@@ -237,7 +240,7 @@ def main():
                                 tflops=round(res["tflops"], 2),
                                 frac_bf16_peak=round(res["tflops"] / BF16_PEAK_TFLOPS, 4),
                                 algorithmic_flops_per_step=res["flops"],
-                                kernels="prefill_schedule_kernel + varlen_prefill_kernel + paged_mq_attn_kernel")
+                                kernels="prefill_schedule_kernel + varlen_prefill_kernel + paged_mq_attn_kernel<2,2> (short-query rows; none here)")
         del pools
         torch.cuda.empty_cache()
 
@@ -249,7 +252,7 @@ def main():
         extra["long_decode"] = dict(workload=wl.name, ms_per_step=round(res["ms"], 5),
                                     gbs=round(res["gbs"], 2), frac_hbm_peak=round(res["gbs"] / HBM_PEAK_GBS, 4),
                                     algorithmic_bytes_per_step=res["bytes"],
-                                    kernels="paged_mq_attn_kernel<1,2> + mq_reduce_kernel")
+                                    kernels="decode_sk_kernel<1,8,QL> + decode_sk_merge_kernel")
         del pools
         torch.cuda.empty_cache()
 

@@ -622,20 +622,21 @@ __global__ __launch_bounds__(256) void mq_reduce_varlen_kernel(MqParams p) {
 // Balanced decode: stream-K over KV stages
 // ---------------------------------------------------------------------------
 // Pure decode (one query row per sequence) with Hkv % 4 == 0.  A pair =
-// (sequence b, group hg of 4 kv heads); its n_b = ceil(L_b / 16) stages of
-// 16 tokens are laid end to end in (b, hg) order, T stages in all.
-// Workgroup w of a persistent grid of W (as many as stay resident) streams
-// stages [w*T/W, (w+1)*T/W), so every workgroup moves the same KV bytes
-// whatever the context lengths; the uneven per-sequence workgroups of
-// paged_mq_attn_kernel leave the machine half idle at the end of a batch.
-// Wave i owns kv head 4*hg + i and all 16 tokens of each stage (one token
-// row slice of 512 bytes per stage row), so no cross-wave merge is needed.
-// A pair inside one range is finished by its workgroup; a pair cut by range
-// boundaries leaves (acc, m, l) per workgroup in the workspace (slot 0: the
-// range's first pair, slot 1: its last) and decode_sk_merge_kernel combines
-// them.  Loads at a pair boundary (query, context length, block-table
-// window) are ordinary loads whose wait also drains the stage pipeline; a
-// workgroup meets one or two boundaries.
+// (sequence b, group hg of HG kv heads, HG = 8 when Hkv % 8 == 0, else 4);
+// its n_b = ceil(L_b / 16) stages of 16 tokens are laid end to end in
+// (b, hg) order, T stages in all.  Workgroup w of a persistent grid of W
+// (as many as stay resident) streams stages [w*T/W, (w+1)*T/W), so every
+// workgroup moves the same KV bytes whatever the context lengths; the
+// uneven per-sequence workgroups of paged_mq_attn_kernel leave the machine
+// half idle at the end of a batch.  Wave i owns kv head HG*hg + i and all
+// 16 tokens of each stage (a 128-byte slice of each token row; with HG = 8
+// a stage row is a whole 1 KiB cache row), so no cross-wave merge is
+// needed.  A pair inside one range is finished by its workgroup; a pair cut
+// by range boundaries leaves (acc, m, l) per workgroup in the workspace
+// (slot 0: the range's first pair, slot 1: its last) and
+// decode_sk_merge_kernel combines them.  Block-table entries and context
+// lengths are scalar loads and, with QL, the queries arrive in LDS with the
+// first stage of each pair, so pair boundaries do not drain the pipeline.
 
 // Wave-uniform read through the scalar data cache (constant address space:
 // the tables are not written while the kernel runs).
@@ -659,6 +660,8 @@ __device__ __forceinline__ int sk_stages(int L) { return L > 0 ? (L + kSkStageTo
 // QL the slot also has room for the queries of the HG kv heads (G <=
 // kSkQMaxG), loaded with the first stage of each pair.
 constexpr int kSkQMaxG = 8;
+constexpr int kSkDepth = 3;            // stages per ring, at most
+constexpr int kSkLdsBytes = 160 * 1024;  // LDS per CU
 template <int HG, bool QL>
 struct SkStage {
   static constexpr int kTS = kSkStageTokens;
@@ -669,7 +672,10 @@ struct SkStage {
   static constexpr int kSlot = kBytes + kQBytes;
   static constexpr int kRowsPerLoad = 8 / HG;
   static constexpr int kLanesPerRow = 8 * HG;
-  static constexpr int kRing = kStages * kSlot;
+  // stages in the ring (kDepth - 1 in flight): kSkDepth, or fewer if the LDS cannot hold them
+  static constexpr int kDepth = kSkDepth * kSlot <= kSkLdsBytes ? kSkDepth : kSkLdsBytes / kSlot;
+  static_assert(kDepth >= 3, "ring of at least three stages");
+  static constexpr int kRing = kDepth * kSlot;
 };
 
 template <int NCB, int HG, bool QL>
@@ -935,15 +941,16 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p) {
     }
   };
 
+  constexpr int D = S::kDepth;
   seek_block();
   begin_pair();
-  issue_stage(0);
-  issue_stage(1);
+#pragma unroll
+  for (int i = 0; i < D - 1; ++i) issue_stage(i);
   for (int s = 0; s < n_w; ++s) {
-    wait_vmcnt<4>();   // this wave's loads of stage s have landed (stage s+1's 4 may not)
-    lds_barrier();     // ... and every wave's; slot (s+2)%3 is no longer being read
-    issue_stage((s + 2) % kStages);
-    const uint8_t* sl = smem + (s % kStages) * S::kSlot;
+    wait_vmcnt<4 * (D - 2)>();  // this wave's loads of stage s have landed (the 4 of each later stage may not)
+    lds_barrier();              // ... and every wave's; slot (s-1)%D is no longer being read
+    issue_stage((s + D - 1) % D);
+    const uint8_t* sl = smem + (s % D) * S::kSlot;
     if (QL && q_from_lds) {
       read_q(sl);
       q_from_lds = false;
