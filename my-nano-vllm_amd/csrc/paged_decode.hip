@@ -260,11 +260,14 @@ __device__ __forceinline__ u32x4 rsrc_words(const void* base, uint32_t num_bytes
 // no memory clobber is declared so the compiler can keep the block-table
 // reads on the scalar path (no kernel code stores to the cache or tables).
 // The M0 write needs no clobber: this code uses M0 only for these loads.
+// The loads are non-temporal (nt): every byte is read once per call, and
+// streaming it past the caches' normal retention measured 10-12% faster
+// for decode (cache lines of the 256 MB-plus KV stream are never reused).
 __device__ __forceinline__ void dma_load16(u32x4 rsrc, uint32_t voff, uint32_t lds) {
   asm volatile(
       "s_mov_b32 m0, %0\n\t"
       "s_nop 0\n\t"
-      "buffer_load_dwordx4 %1, %2, 0 offen lds"
+      "buffer_load_dwordx4 %1, %2, 0 offen nt lds"
       :
       : "s"(lds), "v"(voff), "s"(rsrc));
 }

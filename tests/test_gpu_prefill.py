@@ -84,11 +84,19 @@ def test_prefill_contiguous_equals_paged():
 
 
 def test_prefill_lq1_equals_decode():
+    """Lq = 1 prefill rows (short-query split-KV kernel) against decode (the
+    balanced stream-K kernel at this shape).  Both round P to bf16 against
+    their own running maxima, so they differ by up to a few 1e-3 where the
+    softmax is peaked; each stays within the tolerance of the oracle."""
     announce("prefill: Lq=1 rows equal decode")
     wl = W.qwen3_0p6b_decode(B=24)
-    _, gpu_c = build_pair(wl)
-    q = wl.make_q("cuda")
-    dec = fp8_decode_attention(q, gpu_c[0], gpu_c[1], torch.from_numpy(wl.block_tables).cuda(),
+    cpu_c, gpu_c = build_pair(wl)
+    q = wl.make_q("cpu")
+    dec = fp8_decode_attention(q.cuda(), gpu_c[0], gpu_c[1], torch.from_numpy(wl.block_tables).cuda(),
                                torch.from_numpy(wl.context_lens()).cuda(), SCALE)
-    pre = _prefill_gpu(wl, gpu_c, q)
-    assert torch.equal(dec, pre)
+    pre = _prefill_gpu(wl, gpu_c, q.cuda())
+    want = oa.decode_attention(q, cpu_c[0], cpu_c[1], torch.from_numpy(wl.block_tables),
+                               torch.from_numpy(wl.context_lens()), SCALE)
+    assert_close(dec, want, "decode")
+    assert_close(pre, want, "Lq=1 prefill")
+    assert_close(pre, dec, "Lq=1 prefill vs decode")
