@@ -423,7 +423,12 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
     for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s_cur[rb][i]);
-    mx = fmaxf(mx, shfl_xor_f32(mx, 32)) * p.scale_log2;
+    {  // the other half of the column (lane l ^ 32) through v_permlane32_swap, no LDS round trip
+      const uint32_t u = __builtin_bit_cast(uint32_t, mx);
+      const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+      const uint32_t s0 = sw[0], s1 = sw[1];
+      mx = fmaxf(__builtin_bit_cast(float, s0), __builtin_bit_cast(float, s1)) * p.scale_log2;
+    }
     const bool grow = mx > m_run + kLazyRescaleLog2;  // lazy rescale (see kLazyRescaleLog2)
     if (wave_any(grow)) {
       const float m_new = grow ? mx : m_run;
@@ -437,18 +442,19 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
 
     // exponentials of tile t, two behind each S_{t+1} MFMA: element n of
     // S_t is s_cur[n / 16][n % 16]; word i of the P^T operands holds
-    // elements 2i and 2i + 1.
+    // elements 2i and 2i + 1.  The row sum adds the bf16 weights the PV
+    // MFMAs use, two per v_dot2_f32_bf16 (against 1.0, 1.0).
     uint32_t pw[16];
-    float ps0 = 0.f, ps1 = 0.f;
+    float ps = 0.f;
     qk_mfma(kb_next, s_next, [&](int i) {
       const int rb = i >> 3, n = (2 * i) & 15;
       const float e0 = fast_exp2(__builtin_fmaf(s_cur[rb][n], p.scale_log2, -m_use));
       const float e1 = fast_exp2(__builtin_fmaf(s_cur[rb][n + 1], p.scale_log2, -m_use));
-      ps0 += e0;
-      ps1 += e1;
       pw[i] = pack_bf16x2(e0, e1);
+      ps = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[i]), __builtin_bit_cast(bf16x2, 0x3f803f80u),
+                                           ps, false);
     });
-    l_run += ps0 + ps1;
+    l_run += ps;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) pop[ks] = as_bf16x8(pw[4 * ks], pw[4 * ks + 1], pw[4 * ks + 2], pw[4 * ks + 3]);
     __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
