@@ -240,7 +240,7 @@ def main():
                                 tflops=round(res["tflops"], 2),
                                 frac_bf16_peak=round(res["tflops"] / BF16_PEAK_TFLOPS, 4),
                                 algorithmic_flops_per_step=res["flops"],
-                                kernels="prefill_schedule_kernel + varlen_prefill_kernel + paged_mq_attn_kernel<2,2> (short-query rows; none here)")
+                                kernels="prefill_short_kernel<2,2> (short-query rows, none here, and the work list) + varlen_prefill_kernel")
         del pools
         torch.cuda.empty_cache()
 

@@ -312,62 +312,62 @@ int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, con
                 (long long)need, (long long)workspace_bytes);
 
   // Short-query sequences: split-KV multi-query kernel.
-  {
-    nvamd::MqParams p{};
-    p.q = static_cast<const uint16_t*>(q);
-    p.k = static_cast<const uint8_t*>(k);
-    p.v = static_cast<const uint8_t*>(v);
-    p.block_tables = block_tables;
-    p.bt_stride = paged ? max_num_blocks : 0;
-    p.context_lens = nullptr;
-    p.cu_q = cu_seqlens_q;
-    p.cu_k = cu_seqlens_k;
-    p.out = static_cast<uint16_t*>(out);
-    p.q_rows = num_tokens;
-    p.kv_rows = num_kv_rows;
-    p.num_seqs = num_seqs;
-    p.Hq = num_heads;
-    p.Hkv = num_kv_heads;
-    p.G = G;
-    p.block_size = paged ? block_size : 64;
-    p.part_tokens = (int)part;
-    p.max_parts = (int)ceil_div(kv_cap, part);
-    p.mq_max_q = std::min(mq_max_q, max_seqlen_q);
-    p.scale_log2 = softmax_scale * 1.4426950408889634f;
-    set_partials(p, partials > 0 ? workspace : nullptr);
-    const int ncb = (G * p.mq_max_q + 15) / 16;
-    hipError_t e = nvamd::launch_paged_mq(p, ncb, (hipStream_t)stream);
-    if (e != hipSuccess) return launch_status(e, fn);
-  }
+  nvamd::MqParams mp{};
+  mp.q = static_cast<const uint16_t*>(q);
+  mp.k = static_cast<const uint8_t*>(k);
+  mp.v = static_cast<const uint8_t*>(v);
+  mp.block_tables = block_tables;
+  mp.bt_stride = paged ? max_num_blocks : 0;
+  mp.context_lens = nullptr;
+  mp.cu_q = cu_seqlens_q;
+  mp.cu_k = cu_seqlens_k;
+  mp.out = static_cast<uint16_t*>(out);
+  mp.q_rows = num_tokens;
+  mp.kv_rows = num_kv_rows;
+  mp.num_seqs = num_seqs;
+  mp.Hq = num_heads;
+  mp.Hkv = num_kv_heads;
+  mp.G = G;
+  mp.block_size = paged ? block_size : 64;
+  mp.part_tokens = (int)part;
+  mp.max_parts = (int)ceil_div(kv_cap, part);
+  mp.mq_max_q = std::min(mq_max_q, max_seqlen_q);
+  mp.scale_log2 = softmax_scale * 1.4426950408889634f;
+  set_partials(mp, partials > 0 ? workspace : nullptr);
+  const int ncb = (G * mp.mq_max_q + 15) / 16;
+  if (max_seqlen_q <= mq_max_q)  // short sequences only: the split-KV kernel and its merge
+    return launch_status(nvamd::launch_paged_mq(mp, ncb, (hipStream_t)stream), fn);
 
-  // Longer sequences: MFMA prefill kernel.
-  if (max_seqlen_q > mq_max_q) {
-    nvamd::PrefillParams p{};
-    p.q = static_cast<const uint16_t*>(q);
-    p.k = static_cast<const uint8_t*>(k);
-    p.v = static_cast<const uint8_t*>(v);
-    p.block_tables = block_tables;
-    p.bt_stride = paged ? max_num_blocks : 0;
-    p.cu_q = cu_seqlens_q;
-    p.cu_k = cu_seqlens_k;
-    p.out = static_cast<uint16_t*>(out);
-    p.q_rows = num_tokens;
-    p.kv_rows = num_kv_rows;
-    p.num_seqs = num_seqs;
-    p.Hq = num_heads;
-    p.Hkv = num_kv_heads;
-    p.G = G;
-    p.GW = heads_per_workgroup(G);
-    p.BM = prefill_bm(G);
-    p.n_hgroups = G / p.GW;
-    p.n_mblocks = (int)ceil_div(max_seqlen_q, p.BM);
-    p.block_size = paged ? block_size : 64;
-    p.mq_max_q = mq_max_q;
-    p.scale_log2 = softmax_scale * 1.4426950408889634f;
-    void* schedule = static_cast<char*>(workspace) + align_up(partials);
-    hipError_t e = nvamd::launch_varlen_prefill(p, schedule, (hipStream_t)stream);
-    if (e != hipSuccess) return launch_status(e, fn);
-  }
+  // Longer sequences: MFMA prefill kernel.  Two launches: the short-query
+  // pass (which also writes the prefill work list), then the prefill kernel
+  // (which also merges the short-query partitions).
+  nvamd::PrefillParams pp{};
+  pp.q = static_cast<const uint16_t*>(q);
+  pp.k = static_cast<const uint8_t*>(k);
+  pp.v = static_cast<const uint8_t*>(v);
+  pp.block_tables = block_tables;
+  pp.bt_stride = paged ? max_num_blocks : 0;
+  pp.cu_q = cu_seqlens_q;
+  pp.cu_k = cu_seqlens_k;
+  pp.out = static_cast<uint16_t*>(out);
+  pp.q_rows = num_tokens;
+  pp.kv_rows = num_kv_rows;
+  pp.num_seqs = num_seqs;
+  pp.Hq = num_heads;
+  pp.Hkv = num_kv_heads;
+  pp.G = G;
+  pp.GW = heads_per_workgroup(G);
+  pp.BM = prefill_bm(G);
+  pp.n_hgroups = G / pp.GW;
+  pp.n_mblocks = (int)ceil_div(max_seqlen_q, pp.BM);
+  pp.block_size = paged ? block_size : 64;
+  pp.mq_max_q = mq_max_q;
+  pp.scale_log2 = softmax_scale * 1.4426950408889634f;
+  void* schedule = static_cast<char*>(workspace) + align_up(partials);
+  hipError_t e = nvamd::launch_prefill_short(mp, ncb, pp, schedule, (hipStream_t)stream);
+  if (e != hipSuccess) return launch_status(e, fn);
+  e = nvamd::launch_varlen_prefill(pp, schedule, mp, mp.max_parts > 1, (hipStream_t)stream);
+  if (e != hipSuccess) return launch_status(e, fn);
   return ok();
 }
 

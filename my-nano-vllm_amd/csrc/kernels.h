@@ -75,11 +75,16 @@ hipError_t launch_paged_mq(const MqParams& p, int ncb, hipStream_t stream);
 int decode_sk_wgs_per_cu(int ncb, int hg, int G);
 hipError_t launch_decode_sk(const MqParams& p, int ncb, hipStream_t stream);
 
-// Device bytes of the work list the prefill launch writes (sorted items).
+// Device bytes of the prefill work list (sorted items).
 int64_t prefill_schedule_bytes(const PrefillParams& p);
 
-// Launches the schedule pass and the prefill kernel; `schedule` points to
-// prefill_schedule_bytes(p) bytes of device scratch.
-hipError_t launch_varlen_prefill(const PrefillParams& p, void* schedule, hipStream_t stream);
+// Short-query (split-KV) pass of a prefill call whose extra workgroup writes
+// the prefill work list to `items` (prefill_schedule_bytes(pp) bytes).
+hipError_t launch_prefill_short(const MqParams& p, int ncb, const PrefillParams& pp, void* items, hipStream_t stream);
+
+// The prefill kernel over the work list `schedule`; with `merge`, extra
+// workgroups also merge the short-query pass's partitions (mq).
+hipError_t launch_varlen_prefill(const PrefillParams& p, const void* schedule, const MqParams& mq, bool merge,
+                                 hipStream_t stream);
 
 }  // namespace nvamd

@@ -41,6 +41,8 @@
 
 #include "fp8_common.h"
 #include "kernels.h"
+#include "mq_merge.h"
+#include "prefill_items.h"
 
 namespace nvamd {
 
@@ -171,13 +173,6 @@ struct SeqGeom {
   bool active;
 };
 
-// Keys a sequence can address: at most max_parts partitions and, for the
-// paged layout, at most the block-table width (the reference's loop bound).
-__device__ __forceinline__ int key_capacity(const MqParams& p) {
-  int64_t cap = (int64_t)p.max_parts * p.part_tokens;
-  if (p.block_tables != nullptr) cap = min(cap, p.bt_stride * (int64_t)p.block_size);
-  return (int)min(cap, (int64_t)0x7fffffff);
-}
 
 __device__ __forceinline__ SeqGeom seq_geom(const MqParams& p, int seq) {
   SeqGeom sg;
@@ -298,15 +293,14 @@ __device__ __forceinline__ void lds_barrier() {
 
 }  // namespace
 
+// Work item (partition `part`, kv head group `hg`: heads hg*HG .. hg*HG+HG-1,
+// sequence `seq`) of the split-KV kernel.
 template <int NCB, int HG>
-__global__ __launch_bounds__(256) void paged_mq_attn_kernel(MqParams p) {
+__device__ __forceinline__ void mq_attn(const MqParams& p, const int part, const int hg, const int seq) {
   using S = Stage<HG>;
   __shared__ __attribute__((aligned(16))) uint8_t smem[kRingBytes];
   const uint32_t lds_smem = wave_uniform((int)lds_addr(smem));
 
-  const int part = blockIdx.x;
-  const int hg = blockIdx.y;            // kv head group: heads hg*HG .. hg*HG+HG-1
-  const int seq = blockIdx.z;
   const SeqGeom sg = seq_geom(p, seq);
   if (!sg.active) return;
   const int tid = threadIdx.x;
@@ -566,35 +560,22 @@ __global__ __launch_bounds__(256) void paged_mq_attn_kernel(MqParams p) {
   }
 }
 
-// Log-sum-exp merge of the partitions of one (query row, head) by one wave.
-__device__ __forceinline__ void merge_partitions(const MqParams& p, int64_t rh, int Lk, int lane) {
-  Lk = min(Lk, key_capacity(p));
-  if (Lk <= 0) return;
-  const int n_parts = (Lk + p.part_tokens - 1) / p.part_tokens;
-  if (n_parts <= 1) return;
+template <int NCB, int HG>
+__global__ __launch_bounds__(256) void paged_mq_attn_kernel(MqParams p) {
+  mq_attn<NCB, HG>(p, blockIdx.x, blockIdx.y, blockIdx.z);
+}
 
-  const float* ml = p.part_ml + 2 * rh * p.max_parts;
-  float M = -INFINITY;
-  for (int q = lane; q < n_parts; q += 64) M = fmaxf(M, ml[2 * q]);
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, shfl_xor_f32(M, off));
-  const float Ms = (M == -INFINITY) ? 0.f : M;
-  float L = 0.f;
-  for (int q = lane; q < n_parts; q += 64) L += ml[2 * q + 1] * fast_exp2(ml[2 * q] - Ms);
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) L += shfl_xor_f32(L, off);
-
-  const float* pa = p.part_acc + rh * p.max_parts * kHeadDim + 2 * lane;
-  float o0 = 0.f, o1 = 0.f;
-  for (int q = 0; q < n_parts; ++q) {
-    const float w = fast_exp2(ml[2 * q] - Ms);
-    const f32x2 a = *reinterpret_cast<const f32x2*>(pa + (int64_t)q * kHeadDim);
-    o0 += w * a.x;
-    o1 += w * a.y;
+// Short-query pass of a prefill call, with one more z-slice whose first
+// workgroup writes the prefill kernel's work list (the prefill kernel is the
+// next launch on the stream).
+template <int NCB, int HG>
+__global__ __launch_bounds__(256) void prefill_short_kernel(MqParams p, PrefillParams pp, int2* items,
+                                                            int n_items_max) {
+  if ((int)blockIdx.z == p.num_seqs) {
+    if (blockIdx.x == 0 && blockIdx.y == 0) prefill_schedule(pp, items, n_items_max);
+    return;
   }
-  const float inv = (L > 0.f) ? 1.0f / L : 0.f;
-  const uint32_t w = out_round_bf16_bits(o0 * inv) | (out_round_bf16_bits(o1 * inv) << 16);
-  *reinterpret_cast<uint32_t*>(p.out + rh * kHeadDim + 2 * lane) = w;
+  mq_attn<NCB, HG>(p, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
 // Decode mode: one wave per (sequence, head).
@@ -605,20 +586,9 @@ __global__ __launch_bounds__(256) void mq_reduce_kernel(MqParams p) {
   merge_partitions(p, rh, p.context_lens[rh / p.Hq], lane);
 }
 
-// Varlen mode: one workgroup per sequence; only short-query sequences (the
-// ones the split-KV kernel served) have partitions to merge.
+// Varlen mode: one workgroup per sequence.
 __global__ __launch_bounds__(256) void mq_reduce_varlen_kernel(MqParams p) {
-  const int seq = blockIdx.x;
-  const int row0 = p.cu_q[seq];
-  const int Lq = p.cu_q[seq + 1] - row0;
-  if (Lq <= 0 || Lq > p.mq_max_q) return;
-  const int Lk = p.cu_k[seq + 1] - p.cu_k[seq];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int idx = wave; idx < Lq * p.Hq; idx += 4) {
-    const int64_t row = (int64_t)row0 + idx / p.Hq;
-    if (row >= p.q_rows) break;
-    merge_partitions(p, row * p.Hq + idx % p.Hq, Lk, lane);
-  }
+  merge_varlen_seq(p, blockIdx.x, threadIdx.x >> 6, 4, threadIdx.x & 63);
 }
 
 // ---------------------------------------------------------------------------
@@ -1108,6 +1078,25 @@ hipError_t launch_decode_sk(const MqParams& p, int ncb, hipStream_t stream) {
   if (e != hipSuccess) return e;
   const int64_t waves = (int64_t)p.num_seqs * p.Hq;
   hipLaunchKernelGGL(decode_sk_merge_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_prefill_short(const MqParams& p, int ncb, const PrefillParams& pp, void* items,
+                                hipStream_t stream) {
+  if (p.num_seqs == 0 || items == nullptr) return hipErrorInvalidValue;
+  const int64_t n_items_max = (int64_t)pp.num_seqs * pp.n_mblocks;
+  if (n_items_max > 0x7fffffff) return hipErrorInvalidValue;
+  const int hg = (p.Hkv % 2 == 0) ? 2 : 1;  // kv heads per workgroup
+  const dim3 grid((unsigned)p.max_parts, (unsigned)(p.Hkv / hg), (unsigned)p.num_seqs + 1u);
+  int2* it = static_cast<int2*>(items);
+  const int n = (int)n_items_max;
+  switch (2 * (ncb - 1) + (hg - 1)) {
+    case 0: hipLaunchKernelGGL((prefill_short_kernel<1, 1>), grid, dim3(256), 0, stream, p, pp, it, n); break;
+    case 1: hipLaunchKernelGGL((prefill_short_kernel<1, 2>), grid, dim3(256), 0, stream, p, pp, it, n); break;
+    case 2: hipLaunchKernelGGL((prefill_short_kernel<2, 1>), grid, dim3(256), 0, stream, p, pp, it, n); break;
+    case 3: hipLaunchKernelGGL((prefill_short_kernel<2, 2>), grid, dim3(256), 0, stream, p, pp, it, n); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

@@ -10,10 +10,12 @@
 // Work item = (sequence, m-block of BM query tokens) x (kv head, group of GW
 // query heads sharing it).  A workgroup is 8 waves = 256 query rows = GW
 // heads x BM tokens; wave w owns 32 rows: head (w % GW), tokens
-// [m0 + 32*(w / GW), +32).  prefill_schedule_kernel first orders the items
-// by decreasing number of KV tiles (a counting sort on the device), and the
-// grid walks that list with the kv-head group varying fastest, so the
-// longest items start first and short ones fill the tail.
+// [m0 + 32*(w / GW), +32).  The short-query launch before this kernel
+// orders the items by decreasing number of KV tiles (a counting sort on the
+// device, prefill_schedule), and the grid walks that list with the kv-head
+// group varying fastest, so the longest items start first and short ones
+// fill the tail.  Workgroups past the items merge the short-query rows'
+// split-KV partitions.
 //
 // K/V stream in 64-token tiles, K one tile ahead of V.  Waves 0..3 load and
 // stage K tiles, waves 4..7 V tiles: each thread loads its share of an FP8
@@ -42,19 +44,20 @@
 // register-budgeted for two waves per SIMD (one workgroup per CU).
 #include "fp8_common.h"
 #include "kernels.h"
+#include "mq_merge.h"
+#include "prefill_items.h"
 
 namespace nvamd {
 
 namespace {
 
-constexpr int kBN = 64;                       // kv tokens per tile
+constexpr int kBN = kPrefillTile;             // kv tokens per tile
 constexpr int kKPitch = kHeadDim + 8;         // bf16 per K row in LDS (272 B)
 constexpr int kVPitch = kBN + 8;              // bf16 per V^T row in LDS (144 B)
 constexpr int kKElems = kBN * kKPitch;        // 8704
 constexpr int kVElems = kHeadDim * kVPitch;   // 9216
 constexpr int kBufElems = kKElems + kVElems;  // 17920 bf16 = 35840 B per K + V pair
 constexpr int kBtWindow = 64;                 // block-table entries held in one register
-constexpr int kCostBuckets = 1024;            // schedule sort resolution (tiles)
 
 // One staging thread's share of a K or V tile (see the staging geometry in
 // the kernel): K rows s/8 (r[0], r[1]) and s/8 + 32 (r[2], r[3]), bytes
@@ -92,96 +95,23 @@ __device__ __forceinline__ void lds_store8(const uint16_t* p, u32x2 v) {
 // s_waitcnt lgkmcnt(0): every LDS access of this wave has completed.
 __device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xc07f); }
 
-struct ItemGeom {
-  int q_start, Lq, k_start, Lk, c;
-};
-
-__device__ __forceinline__ ItemGeom item_geom(const PrefillParams& p, int seq) {
-  ItemGeom g;
-  g.q_start = p.cu_q[seq];
-  g.Lq = p.cu_q[seq + 1] - g.q_start;
-  g.k_start = p.cu_k[seq];
-  g.Lk = p.cu_k[seq + 1] - g.k_start;
-  g.c = g.Lk - g.Lq;
-  return g;
-}
-
-// KV tiles item (seq, mb) visits: keys visible to the block's last row,
-// bounded by the block table.
-__device__ __forceinline__ int item_tiles(const PrefillParams& p, const ItemGeom& g, int mb) {
-  int kv_hi = min(g.Lk, g.c + mb * p.BM + p.BM);
-  if (p.block_tables != nullptr) kv_hi = (int)min((int64_t)kv_hi, p.bt_stride * (int64_t)p.block_size);
-  return max(0, (kv_hi + kBN - 1) / kBN);
-}
-
-__device__ __forceinline__ bool item_valid(const PrefillParams& p, const ItemGeom& g, int mb) {
-  return g.Lq > p.mq_max_q && mb * p.BM < g.Lq;
-}
-
 }  // namespace
-
-// ---------------------------------------------------------------------------
-// Schedule: one workgroup writes the (seq, m-block) items in decreasing tile
-// count (counting sort), followed by (-1, -1) for slots without an item.
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void prefill_schedule_kernel(PrefillParams p, int2* __restrict__ items,
-                                                               int n_items_max) {
-  __shared__ int hist[kCostBuckets];
-  __shared__ int warp_tot[4];
-  const int tid = threadIdx.x;
-  for (int b = tid; b < kCostBuckets; b += 256) hist[b] = 0;
-  __syncthreads();
-  for (int idx = tid; idx < n_items_max; idx += 256) {
-    const int seq = idx / p.n_mblocks, mb = idx - seq * p.n_mblocks;
-    const ItemGeom g = item_geom(p, seq);
-    if (!item_valid(p, g, mb)) continue;
-    atomicAdd(&hist[min(item_tiles(p, g, mb), kCostBuckets - 1)], 1);
-  }
-  __syncthreads();
-  // Exclusive scan in decreasing cost order: thread t owns buckets
-  // [1023 - 4t - 3, 1023 - 4t] (walked from high cost to low).
-  int local[4], sum = 0;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    local[j] = hist[kCostBuckets - 1 - (4 * tid + j)];
-    sum += local[j];
-  }
-  int incl = sum;  // inclusive scan of per-thread sums over the wave
-  const int lane = tid & 63, wave = tid >> 6;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int o = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += o;
-  }
-  if (lane == 63) warp_tot[wave] = incl;
-  __syncthreads();
-  int base = 0;
-  for (int w = 0; w < wave; ++w) base += warp_tot[w];
-  const int total = warp_tot[0] + warp_tot[1] + warp_tot[2] + warp_tot[3];
-  int run = base + incl - sum;
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    hist[kCostBuckets - 1 - (4 * tid + j)] = run;
-    run += local[j];
-  }
-  __syncthreads();
-  for (int idx = tid; idx < n_items_max; idx += 256) {
-    const int seq = idx / p.n_mblocks, mb = idx - seq * p.n_mblocks;
-    const ItemGeom g = item_geom(p, seq);
-    if (!item_valid(p, g, mb)) continue;
-    const int pos = atomicAdd(&hist[min(item_tiles(p, g, mb), kCostBuckets - 1)], 1);
-    items[pos] = make_int2(seq, mb);
-  }
-  for (int pos = total + tid; pos < n_items_max; pos += 256) items[pos] = make_int2(-1, -1);
-}
 
 // ---------------------------------------------------------------------------
 // Main kernel
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(PrefillParams p,
-                                                                              const int2* __restrict__ items) {
+                                                                              const int2* __restrict__ items,
+                                                                              MqParams mq, int n_main) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kBufElems];
+
+  // Workgroups past the items merge the split-KV partitions of the
+  // short-query sequences (one sequence each), which the launch before this
+  // one computed.
+  if ((int)blockIdx.x >= n_main) {
+    merge_varlen_seq(mq, (int)blockIdx.x - n_main, wave_uniform(threadIdx.x >> 6), kPrefillWaves, threadIdx.x & 63);
+    return;
+  }
 
   // blockIdx.x = item * n_groups + group: the kv-head group varies fastest.
   const int n_groups = p.Hkv * p.n_hgroups;
@@ -238,6 +168,10 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
   // stores (one dim row, 4 tokens each) land on 16 distinct bank pairs;
   // each load instruction still covers 4 whole rows.
   const bool k_role = wave < 4;
+  // The V waves stage twice the vector work of the K waves (the transpose)
+  // and, being younger, lose the SIMD's issue arbitration to them, so they
+  // reach each barrier last; a higher wave priority evens that out.
+  if (!k_role) __builtin_amdgcn_s_setprio(1);
   const int stid = tid & 255;
   const int k_row = stid >> 3;                      // K rows k_row and k_row + 32
   const int k_byte = 16 * (stid & 7);
@@ -547,17 +481,15 @@ int64_t prefill_schedule_bytes(const PrefillParams& p) {
   return (int64_t)p.num_seqs * p.n_mblocks * (int64_t)sizeof(int2);
 }
 
-hipError_t launch_varlen_prefill(const PrefillParams& p, void* schedule, hipStream_t stream) {
+hipError_t launch_varlen_prefill(const PrefillParams& p, const void* schedule, const MqParams& mq, bool merge,
+                                 hipStream_t stream) {
   if (p.num_seqs == 0 || p.n_mblocks == 0) return hipSuccess;
   const int64_t n_items_max = (int64_t)p.num_seqs * p.n_mblocks;
   const int64_t n_blocks = n_items_max * p.Hkv * p.n_hgroups;
-  if (n_blocks > 0x7fffffff || schedule == nullptr) return hipErrorInvalidValue;
-  int2* items = static_cast<int2*>(schedule);
-  hipLaunchKernelGGL(prefill_schedule_kernel, dim3(1), dim3(256), 0, stream, p, items, (int)n_items_max);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(varlen_prefill_kernel, dim3((unsigned)n_blocks), dim3(64 * kPrefillWaves), 0, stream, p,
-                     (const int2*)items);
+  const int64_t n_merge = merge ? mq.num_seqs : 0;
+  if (n_blocks + n_merge > 0x7fffffff || schedule == nullptr) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(varlen_prefill_kernel, dim3((unsigned)(n_blocks + n_merge)), dim3(64 * kPrefillWaves), 0, stream,
+                     p, static_cast<const int2*>(schedule), mq, (int)n_blocks);
   return hipGetLastError();
 }
 
