@@ -361,6 +361,7 @@ int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, con
   pp.n_hgroups = G / pp.GW;
   pp.n_mblocks = (int)ceil_div(max_seqlen_q, pp.BM);
   pp.block_size = paged ? block_size : 64;
+  pp.bs_shift = (pp.block_size & (pp.block_size - 1)) == 0 ? __builtin_ctz((unsigned)pp.block_size) : -1;
   pp.mq_max_q = mq_max_q;
   pp.scale_log2 = softmax_scale * 1.4426950408889634f;
   void* schedule = static_cast<char*>(workspace) + align_up(partials);

@@ -61,6 +61,7 @@ struct PrefillParams {
   int n_hgroups;  // G / GW
   int n_mblocks;  // ceil(max_seqlen_q / BM)
   int block_size;
+  int bs_shift;   // log2(block_size) when it is a power of two, else -1
   int mq_max_q;   // sequences with Lq <= mq_max_q are left to the short-query kernel
   float scale_log2;
 };

@@ -197,7 +197,9 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
     int nvalid = (t < n_tiles) ? min(kBN, Lk - kv0) : 0;
     int64_t row0 = 0;
     if (paged) {
-      const int bi = kv0 / p.block_size;
+      // block index and offset: shift and mask for power-of-two block sizes
+      // (a runtime division costs dozens of instructions per tile)
+      const int bi = (p.bs_shift >= 0) ? (kv0 >> p.bs_shift) : kv0 / p.block_size;
       const int blk = __builtin_amdgcn_readlane(bt_lane, min(max(bi - win_base, 0), kBtWindow - 1));
       row0 = (int64_t)blk * p.block_size + (kv0 - bi * p.block_size);
       if (blk < 0 || row0 + kBN > p.kv_rows) nvalid = 0;
