@@ -100,3 +100,14 @@ def test_prefill_lq1_equals_decode():
     assert_close(dec, want, "decode")
     assert_close(pre, want, "Lq=1 prefill")
     assert_close(pre, dec, "Lq=1 prefill vs decode")
+
+
+@pytest.mark.parametrize("bs", [64, 192, 512])
+def test_prefill_block_sizes(bs):
+    """Block sizes other than 256: powers of two take the shift path of the
+    tile addressing, 192 the division path; chunks cross many block borders."""
+    rng = np.random.default_rng(bs)
+    seqs = [W.SeqSpec(lq=int(l), cached=int(rng.integers(0, 900))) for l in (300, 129, 64, 7, 512)]
+    wl = W.make_workload(f"prefill_bs{bs}", 32, 8, seqs, seed=int(rng.integers(1 << 30)), block_size=bs)
+    announce(f"prefill: block_size {bs}")
+    _check(wl)
