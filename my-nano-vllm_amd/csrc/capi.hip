@@ -134,12 +134,14 @@ int64_t align_up(int64_t n) { return (n + 255) / 256 * 256; }
 // Prefill kernel geometry for G query heads per kv head.
 int prefill_bm(int g) { return 32 * nvamd::kPrefillWaves / heads_per_workgroup(g); }
 
+constexpr int64_t kPrefillItemBytes = 32;  // sizeof(nvamd::PrefillItem)
+
 // Bytes of the prefill work list (0 when every sequence takes the
 // short-query path).
 int64_t schedule_bytes(int32_t num_seqs, int g, int32_t max_seqlen_q) {
   const int mq_max_q = kMqMaxCols / g;
   if (max_seqlen_q <= mq_max_q) return 0;
-  return (int64_t)num_seqs * ceil_div(max_seqlen_q, prefill_bm(g)) * 8;
+  return (int64_t)num_seqs * ceil_div(max_seqlen_q, prefill_bm(g)) * kPrefillItemBytes;
 }
 
 }  // namespace
@@ -361,7 +363,8 @@ int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, con
   pp.n_hgroups = G / pp.GW;
   pp.n_mblocks = (int)ceil_div(max_seqlen_q, pp.BM);
   pp.block_size = paged ? block_size : 64;
-  pp.bs_shift = (pp.block_size & (pp.block_size - 1)) == 0 ? __builtin_ctz((unsigned)pp.block_size) : -1;
+  pp.tpb = pp.block_size / 64;
+  pp.tpb_magic = (uint32_t)(((1u << 31) - 1u) / (uint32_t)pp.tpb + 1u);
   pp.mq_max_q = mq_max_q;
   pp.scale_log2 = softmax_scale * 1.4426950408889634f;
   void* schedule = static_cast<char*>(workspace) + align_up(partials);

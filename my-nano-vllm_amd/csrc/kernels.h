@@ -61,7 +61,8 @@ struct PrefillParams {
   int n_hgroups;  // G / GW
   int n_mblocks;  // ceil(max_seqlen_q / BM)
   int block_size;
-  int bs_shift;   // log2(block_size) when it is a power of two, else -1
+  int tpb;            // 64-token tiles per block (block_size / 64)
+  uint32_t tpb_magic;  // ceil(2^31 / tpb): block of tile t = umulhi(2t, tpb_magic)
   int mq_max_q;   // sequences with Lq <= mq_max_q are left to the short-query kernel
   float scale_log2;
 };
@@ -83,8 +84,9 @@ int64_t prefill_schedule_bytes(const PrefillParams& p);
 // the prefill work list to `items` (prefill_schedule_bytes(pp) bytes).
 hipError_t launch_prefill_short(const MqParams& p, int ncb, const PrefillParams& pp, void* items, hipStream_t stream);
 
-// The prefill kernel over the work list `schedule`; with `merge`, extra
-// workgroups also merge the short-query pass's partitions (mq).
+// The prefill kernel over the work list `schedule` (one workgroup per work
+// unit); with `merge`, extra workgroups also merge the short-query pass's
+// partitions (mq).
 hipError_t launch_varlen_prefill(const PrefillParams& p, const void* schedule, const MqParams& mq, bool merge,
                                  hipStream_t stream);
 

@@ -569,7 +569,7 @@ __global__ __launch_bounds__(256) void paged_mq_attn_kernel(MqParams p) {
 // workgroup writes the prefill kernel's work list (the prefill kernel is the
 // next launch on the stream).
 template <int NCB, int HG>
-__global__ __launch_bounds__(256) void prefill_short_kernel(MqParams p, PrefillParams pp, int2* items,
+__global__ __launch_bounds__(256) void prefill_short_kernel(MqParams p, PrefillParams pp, PrefillItem* items,
                                                             int n_items_max) {
   if ((int)blockIdx.z == p.num_seqs) {
     if (blockIdx.x == 0 && blockIdx.y == 0) prefill_schedule(pp, items, n_items_max);
@@ -1088,7 +1088,7 @@ hipError_t launch_prefill_short(const MqParams& p, int ncb, const PrefillParams&
   if (n_items_max > 0x7fffffff) return hipErrorInvalidValue;
   const int hg = (p.Hkv % 2 == 0) ? 2 : 1;  // kv heads per workgroup
   const dim3 grid((unsigned)p.max_parts, (unsigned)(p.Hkv / hg), (unsigned)p.num_seqs + 1u);
-  int2* it = static_cast<int2*>(items);
+  PrefillItem* it = static_cast<PrefillItem*>(items);
   const int n = (int)n_items_max;
   switch (2 * (ncb - 1) + (hg - 1)) {
     case 0: hipLaunchKernelGGL((prefill_short_kernel<1, 1>), grid, dim3(256), 0, stream, p, pp, it, n); break;

@@ -15,6 +15,14 @@ struct ItemGeom {
   int q_start, Lq, k_start, Lk, c;
 };
 
+// One entry of the prefill work list: a (sequence, m-block) item with its
+// geometry resolved, so that a workgroup needs a single load to start it.
+// seq < 0 marks a slot past the last item.
+// head = {seq, mb, q_start, Lq}, tail = {k_start, Lk, n_tiles, 0}.
+struct PrefillItem {
+  int4 head, tail;
+};
+
 __device__ __forceinline__ ItemGeom item_geom(const PrefillParams& p, int seq) {
   ItemGeom g;
   g.q_start = p.cu_q[seq];
@@ -39,9 +47,10 @@ __device__ __forceinline__ bool item_valid(const PrefillParams& p, const ItemGeo
 
 // Work list of the prefill kernel: one 256-thread workgroup writes the
 // (seq, m-block) items in decreasing tile count (counting sort), followed by
-// (-1, -1) for slots without an item.  Run as an extra workgroup of the
-// short-query launch that precedes the prefill kernel.
-__device__ __forceinline__ void prefill_schedule(const PrefillParams& p, int2* __restrict__ items, int n_items_max) {
+// records with seq = -1 for slots without an item.  Run as an extra
+// workgroup of the short-query launch that precedes the prefill kernel.
+__device__ __forceinline__ void prefill_schedule(const PrefillParams& p, PrefillItem* __restrict__ items,
+                                                 int n_items_max) {
   __shared__ int hist[kCostBuckets];
   __shared__ int warp_tot[4];
   const int tid = threadIdx.x;
@@ -86,10 +95,12 @@ __device__ __forceinline__ void prefill_schedule(const PrefillParams& p, int2* _
     const int seq = idx / p.n_mblocks, mb = idx - seq * p.n_mblocks;
     const ItemGeom g = item_geom(p, seq);
     if (!item_valid(p, g, mb)) continue;
-    const int pos = atomicAdd(&hist[min(item_tiles(p, g, mb), kCostBuckets - 1)], 1);
-    items[pos] = make_int2(seq, mb);
+    const int tiles = item_tiles(p, g, mb);
+    const int pos = atomicAdd(&hist[min(tiles, kCostBuckets - 1)], 1);
+    items[pos] = PrefillItem{make_int4(seq, mb, g.q_start, g.Lq), make_int4(g.k_start, g.Lk, tiles, 0)};
   }
-  for (int pos = total + tid; pos < n_items_max; pos += 256) items[pos] = make_int2(-1, -1);
+  for (int pos = total + tid; pos < n_items_max; pos += 256)
+    items[pos] = PrefillItem{make_int4(-1, 0, 0, 0), make_int4(0, 0, 0, 0)};
 }
 
 }  // namespace nvamd

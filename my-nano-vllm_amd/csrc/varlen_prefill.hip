@@ -42,6 +42,8 @@
 // Step t of a wave runs the softmax of S_t with the MFMAs of S_{t+1}
 // interleaved between its exponentials, then O += P_t V_t.  The kernel is
 // register-budgeted for two waves per SIMD (one workgroup per CU).
+#include <type_traits>
+
 #include "fp8_common.h"
 #include "kernels.h"
 #include "mq_merge.h"
@@ -58,6 +60,7 @@ constexpr int kKElems = kBN * kKPitch;        // 8704
 constexpr int kVElems = kHeadDim * kVPitch;   // 9216
 constexpr int kBufElems = kKElems + kVElems;  // 17920 bf16 = 35840 B per K + V pair
 constexpr int kBtWindow = 64;                 // block-table entries held in one register
+constexpr int kLead = 4;                      // MFMA operands are read from LDS this many MFMAs ahead
 
 // One staging thread's share of a K or V tile (see the staging geometry in
 // the kernel): K rows s/8 (r[0], r[1]) and s/8 + 32 (r[2], r[3]), bytes
@@ -95,13 +98,20 @@ __device__ __forceinline__ void lds_store8(const uint16_t* p, u32x2 v) {
 // s_waitcnt lgkmcnt(0): every LDS access of this wave has completed.
 __device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xc07f); }
 
+// Pins a value to this point of the instruction stream: the compiler would
+// otherwise sink a computation into the block of its only use, out of the
+// stretch of MFMAs it is placed between.
+template <typename T>
+__device__ __forceinline__ void pin(T& v) { asm volatile("" : "+v"(v)); }
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
 // Main kernel
 // ---------------------------------------------------------------------------
+template <bool PAGED>
 __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(PrefillParams p,
-                                                                              const int2* __restrict__ items,
+                                                                              const PrefillItem* __restrict__ items,
                                                                               MqParams mq, int n_main) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kBufElems];
 
@@ -117,13 +127,15 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
   const int n_groups = p.Hkv * p.n_hgroups;
   const int item = (int)(blockIdx.x / (unsigned)n_groups);
   const int grp = (int)blockIdx.x - item * n_groups;
-  const int2 it = items[item];
-  if (it.x < 0) return;
-  const int seq = it.x, mb = it.y;
+  // one record load gives the item and its geometry
+  const int4 rec_a = items[item].head, rec_b = items[item].tail;
+  const int seq = wave_uniform(rec_a.x);
+  if (seq < 0) return;
+  const int mb = wave_uniform(rec_a.y), q_start = wave_uniform(rec_a.z), Lq = wave_uniform(rec_a.w);
+  const int k_start = wave_uniform(rec_b.x), Lk = wave_uniform(rec_b.y), n_tiles = wave_uniform(rec_b.z);
+  const int c = Lk - Lq;
   const int g = grp / p.n_hgroups;
   const int hg = grp - g * p.n_hgroups;
-  const ItemGeom geo = item_geom(p, seq);
-  const int Lq = geo.Lq, Lk = geo.Lk, c = geo.c;
   const int m0 = mb * p.BM;
 
   const int tid = threadIdx.x;
@@ -134,18 +146,18 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
   const int m0w = m0 + 32 * tw;          // first query token of this wave
   const int tq = m0w + col;              // this lane's query token
 
-  // ---- Q operand (B of S^T): dims 16ks + 8h + [0,8) --------------------------
+  // ---- Q operand (B of S^T): dims 16ks + 8h + [0,8); rows past the sequence
+  // (or past q) read as zero through a bounded buffer descriptor, no branches
   bf16x8 qop[8];
   {
-    const int64_t row = (int64_t)geo.q_start + tq;
-    const bool valid = tq < Lq && row < p.q_rows;
-    const uint16_t* qp = p.q + (row * p.Hq + head) * kHeadDim + 8 * h;
+    const int64_t row = (int64_t)q_start + m0w;
+    const uint32_t rows = (uint32_t)max<int64_t>(0, min<int64_t>(min(Lq - m0w, 32), p.q_rows - row));
+    const uint32_t row_bytes = (uint32_t)(p.Hq * kHeadDim * 2);
+    const __amdgpu_buffer_rsrc_t qr =
+        make_rsrc(p.q + (row * p.Hq + head) * kHeadDim, rows == 0 ? 0u : (rows - 1) * row_bytes + kHeadDim * 2);
+    const uint32_t qoff = (uint32_t)col * row_bytes + 16 * h;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      u32x4 a = {0u, 0u, 0u, 0u};
-      if (valid) a = *reinterpret_cast<const u32x4*>(qp + 16 * ks);
-      qop[ks] = as_bf16x8(a);
-    }
+    for (int ks = 0; ks < 8; ++ks) qop[ks] = as_bf16x8(buf_load16(qr, qoff + 32 * ks));
   }
 
   f32x16 acc[4];
@@ -153,10 +165,11 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
   for (int db = 0; db < 4; ++db)
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[db][i] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;
+  // Online softmax state: reference maximum (log2 units), the maximum the
+  // exponentials of the current tile use, running row sum, and the row sum
+  // of the next tile's weights computed so far.
+  float m_run = -INFINITY, m_use = 0.f, l_run = 0.f, ps_pend = 0.f;
 
-  const int n_tiles = item_tiles(p, geo, mb);
-  const bool paged = p.block_tables != nullptr;
   const int64_t rs = (int64_t)p.Hkv * kHeadDim;  // bytes between token rows
 
   // ---- per-thread load / staging geometry ------------------------------------
@@ -196,15 +209,16 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
     const int kv0 = t * kBN;
     int nvalid = (t < n_tiles) ? min(kBN, Lk - kv0) : 0;
     int64_t row0 = 0;
-    if (paged) {
-      // block index and offset: shift and mask for power-of-two block sizes
-      // (a runtime division costs dozens of instructions per tile)
-      const int bi = (p.bs_shift >= 0) ? (kv0 >> p.bs_shift) : kv0 / p.block_size;
+    if constexpr (PAGED) {
+      // block of tile t by a multiply with the reciprocal of the tiles per
+      // block (exact for t < 2^31 / tpb; a division would be dozens of
+      // instructions and a branch)
+      const int bi = (int)__umulhi((uint32_t)t << 1, p.tpb_magic);
       const int blk = __builtin_amdgcn_readlane(bt_lane, min(max(bi - win_base, 0), kBtWindow - 1));
-      row0 = (int64_t)blk * p.block_size + (kv0 - bi * p.block_size);
+      row0 = (int64_t)blk * p.block_size + (t - bi * p.tpb) * kBN;
       if (blk < 0 || row0 + kBN > p.kv_rows) nvalid = 0;
     } else {
-      row0 = (int64_t)geo.k_start + kv0;
+      row0 = (int64_t)k_start + kv0;
       if (row0 < 0 || row0 + max(nvalid, 0) > p.kv_rows) nvalid = 0;
     }
     nvalid = max(nvalid, 0);
@@ -214,10 +228,12 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
     return make_rsrc((k_role ? p.k : p.v) + base, nbytes);
   };
   // Loads this thread's share of tile t of its role: K tile t (K waves) or
-  // V tile tv (V waves).
-  auto load = [&](int t, int tv, TileRegs& r) {
-    const __amdgpu_buffer_rsrc_t rs_ = tile_rsrc(k_role ? t : tv);
-    if (k_role) {
+  // V tile tv (V waves).  The role is a compile-time constant (std::true_type
+  // for K) so that no branch splits the code the loads are scheduled into.
+  auto load = [&](auto role, int t, int tv, TileRegs& r) {
+    constexpr bool kRole = decltype(role)::value;
+    const __amdgpu_buffer_rsrc_t rs_ = tile_rsrc(kRole ? t : tv);
+    if constexpr (kRole) {
       r.r[0] = buf_load8(rs_, k_off0);
       r.r[1] = buf_load8(rs_, k_off0 ^ 8u);
       r.r[2] = buf_load8(rs_, k_off1);
@@ -228,183 +244,207 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
     }
   };
 
-  // Converts a K tile share to bf16 and writes it to K buffer kb.
+  // Converts a K tile share to bf16 and writes it to K buffer kb, in four
+  // quarters (one 16-byte store each) that can be spread over a stretch of
+  // MFMAs.
   const int k_lds[2] = {k_row * kKPitch + k_byte + k_first, k_row * kKPitch + k_byte + (k_first ^ 8)};
+  auto stage_k_q = [&](const TileRegs& kr, uint16_t* kb, int i) {
+    const u32x2 w = kr.r[i];
+    u32x4 o;
+    o.x = fp8x2_to_bf16x2<false>(w.x); o.y = fp8x2_to_bf16x2<true>(w.x);
+    o.z = fp8x2_to_bf16x2<false>(w.y); o.w = fp8x2_to_bf16x2<true>(w.y);
+    *reinterpret_cast<u32x4*>(kb + k_lds[i & 1] + (i >> 1) * 32 * kKPitch) = o;
+  };
   auto stage_k = [&](const TileRegs& kr, uint16_t* kb) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const u32x2 w = kr.r[i];
-      u32x4 o;
-      o.x = fp8x2_to_bf16x2<false>(w.x); o.y = fp8x2_to_bf16x2<true>(w.x);
-      o.z = fp8x2_to_bf16x2<false>(w.y); o.w = fp8x2_to_bf16x2<true>(w.y);
-      *reinterpret_cast<u32x4*>(kb + k_lds[i & 1] + (i >> 1) * 32 * kKPitch) = o;
-    }
+    for (int i = 0; i < 4; ++i) stage_k_q(kr, kb, i);
   };
   // Transposes a V tile share (4 tokens x 8 dims) to bf16 and writes it to
-  // V^T buffer vb: one 8-byte store (4 tokens) per dim.
-  // Dims v_byte..v_byte+7 share one chunk swizzle (v_byte is a multiple of
-  // 8), so the 8 stores are one address plus constant offsets.
+  // V^T buffer vb: one 8-byte store (4 tokens) per dim, in four quarters of
+  // two dims each.  Dims v_byte..v_byte+7 share one chunk swizzle (v_byte is
+  // a multiple of 8), so the 8 stores are one address plus constant offsets.
   const int v_lds = v_byte * kVPitch + (v_pos(4 * v_tg) ^ v_swz(v_byte));  // tokens 4tg..4tg+3 stay contiguous
-  auto stage_v = [&](const TileRegs& vr, uint16_t* vb) {
+  // quarter q: dims 2q and 2q + 1 of the share (bytes of the low or high
+  // dword of each token's 8 fp8 for q < 2 or q >= 2)
+  auto stage_v_q = [&](const TileRegs& vr, uint16_t* vb, auto qc) {
+    constexpr int q = decltype(qc)::value;
+    constexpr int half = q >> 1;
     uint16_t* vd = vb + v_lds;
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      const uint32_t a = half ? vr.r[0].y : vr.r[0].x;
-      const uint32_t bb = half ? vr.r[1].y : vr.r[1].x;
-      const uint32_t cc = half ? vr.r[2].y : vr.r[2].x;
-      const uint32_t d = half ? vr.r[3].y : vr.r[3].x;
-      const uint32_t x01 = __builtin_amdgcn_perm(a, bb, 0x01050004u);   // [a0 b0 a1 b1]
-      const uint32_t y01 = __builtin_amdgcn_perm(cc, d, 0x01050004u);   // [c0 d0 c1 d1]
-      const uint32_t x23 = __builtin_amdgcn_perm(a, bb, 0x03070206u);   // [a2 b2 a3 b3]
-      const uint32_t y23 = __builtin_amdgcn_perm(cc, d, 0x03070206u);   // [c2 d2 c3 d3]
-      const uint32_t tt[4] = {__builtin_amdgcn_perm(x01, y01, 0x01000504u),   // [a0 b0 c0 d0]
-                              __builtin_amdgcn_perm(x01, y01, 0x03020706u),   // [a1 b1 c1 d1]
-                              __builtin_amdgcn_perm(x23, y23, 0x01000504u),   // [a2 b2 c2 d2]
-                              __builtin_amdgcn_perm(x23, y23, 0x03020706u)};  // [a3 b3 c3 d3]
-      constexpr int kRow = 2 * kVPitch;  // bytes per V^T row
-      if (half == 0) {
-        lds_store8<0 * kRow>(vd, fp8x4_to_bf16x4(tt[0]));
-        lds_store8<1 * kRow>(vd, fp8x4_to_bf16x4(tt[1]));
-        lds_store8<2 * kRow>(vd, fp8x4_to_bf16x4(tt[2]));
-        lds_store8<3 * kRow>(vd, fp8x4_to_bf16x4(tt[3]));
-      } else {
-        lds_store8<4 * kRow>(vd, fp8x4_to_bf16x4(tt[0]));
-        lds_store8<5 * kRow>(vd, fp8x4_to_bf16x4(tt[1]));
-        lds_store8<6 * kRow>(vd, fp8x4_to_bf16x4(tt[2]));
-        lds_store8<7 * kRow>(vd, fp8x4_to_bf16x4(tt[3]));
-      }
-    }
+    const uint32_t a = half ? vr.r[0].y : vr.r[0].x;
+    const uint32_t bb = half ? vr.r[1].y : vr.r[1].x;
+    const uint32_t cc = half ? vr.r[2].y : vr.r[2].x;
+    const uint32_t d = half ? vr.r[3].y : vr.r[3].x;
+    constexpr uint32_t kSel = (q & 1) ? 0x03070206u : 0x01050004u;  // bytes 2,3 or 0,1 of each token
+    const uint32_t x = __builtin_amdgcn_perm(a, bb, kSel);    // [a_j b_j a_j+1 b_j+1]
+    const uint32_t y = __builtin_amdgcn_perm(cc, d, kSel);    // [c_j d_j c_j+1 d_j+1]
+    const uint32_t t0 = __builtin_amdgcn_perm(x, y, 0x01000504u);  // [a_j b_j c_j d_j]
+    const uint32_t t1 = __builtin_amdgcn_perm(x, y, 0x03020706u);  // [a_j+1 b_j+1 c_j+1 d_j+1]
+    constexpr int kRow = 2 * kVPitch;  // bytes per V^T row
+    lds_store8<(2 * q) * kRow>(vd, fp8x4_to_bf16x4(t0));
+    lds_store8<(2 * q + 1) * kRow>(vd, fp8x4_to_bf16x4(t1));
+  };
+  auto stage_v = [&](const TileRegs& vr, uint16_t* vb) {
+    stage_v_q(vr, vb, std::integral_constant<int, 0>{});
+    stage_v_q(vr, vb, std::integral_constant<int, 1>{});
+    stage_v_q(vr, vb, std::integral_constant<int, 2>{});
+    stage_v_q(vr, vb, std::integral_constant<int, 3>{});
+  };
+  auto stage = [&](auto role, const TileRegs& r, uint16_t* kb, uint16_t* vb) {
+    if constexpr (decltype(role)::value) stage_k(r, kb);
+    else stage_v(r, vb);
+  };
+  // quarter qc (an integral_constant) of the staging
+  auto stage_q = [&](auto role, const TileRegs& r, uint16_t* kb, uint16_t* vb, auto qc) {
+    if constexpr (decltype(role)::value) stage_k_q(r, kb, decltype(qc)::value);
+    else stage_v_q(r, vb, qc);
   };
 
-  // S^T = K . Q^T of one tile (K buffer kb).  The two row blocks' MFMA
-  // chains are interleaved (step i: k-step i/2 of row block i%2); each K
-  // operand is read from LDS four steps before its MFMA.  after(i) runs
-  // behind MFMA i: vector work of another tile that fills the matrix pipe's
-  // shadow.
-  auto qk_mfma = [&](const uint16_t* kb, f32x16 (&s)[2], auto&& after) {
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s[rb][i] = 0.f;
-    const uint16_t* kr = kb + col * kKPitch + 8 * h;
-    auto kaddr = [&](int i) { return kr + (i & 1) * 32 * kKPitch + 16 * (i >> 1); };
-    u32x4 pre[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) pre[i] = *reinterpret_cast<const u32x4*>(kaddr(i));
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const u32x4 cur = pre[i & 3];
-      if (i + 4 < 16) pre[i & 3] = *reinterpret_cast<const u32x4*>(kaddr(i + 4));
-      s[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(cur), qop[i >> 1], s[i & 1], 0, 0, 0);
-      after(i);
-    }
+  // ---- softmax pieces -----------------------------------------------------------
+  // Element n of an S^T tile is s[n / 16][n % 16]; lane (h, col) holds kv
+  // token 32*(n/16) + (n%4) + 8*((n%16)/4) + 4h of query column col.
+  // Word i of the P^T operands holds the weights of elements 2i and 2i + 1;
+  // the row sum adds the bf16 weights the PV MFMAs use, two per
+  // v_dot2_f32_bf16 (against 1.0, 1.0).
+  const bf16x2 ones = __builtin_bit_cast(bf16x2, 0x3f803f80u);
+  auto exp_pair = [&](const f32x16 (&s)[2], int i, uint32_t (&pw)[16], float& ps) {
+    const int rb = i >> 3, n = (2 * i) & 15;
+    const float e0 = fast_exp2(__builtin_fmaf(s[rb][n], p.scale_log2, -m_use));
+    const float e1 = fast_exp2(__builtin_fmaf(s[rb][n + 1], p.scale_log2, -m_use));
+    pw[i] = pack_bf16x2(e0, e1);
+    ps = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[i]), ones, ps, false);
   };
-
-  // O^T += V^T . P^T for one tile (V^T in buffer vb): MFMA i = (k-step i/4,
-  // dim block i%4); each V^T operand is read four MFMAs ahead.
-  auto pv = [&](const bf16x8 (&pp)[4], const uint16_t* vb) {
-    auto vaddr = [&](int i) {
-      const int ks = i >> 2, d = 32 * (i & 3) + col;
-      return vb + d * kVPitch + ((16 * ks + 8 * h) ^ v_swz(d));
-    };
-    u32x4 pre[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) pre[i] = *reinterpret_cast<const u32x4*>(vaddr(i));
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const u32x4 cur = pre[i & 3];
-      if (i + 4 < 16) pre[i & 3] = *reinterpret_cast<const u32x4*>(vaddr(i + 4));
-      acc[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(cur), pp[i >> 2], acc[i & 3], 0, 0, 0);
-    }
-    // keep the reads four MFMAs ahead (the scheduler would otherwise sink
-    // them next to their MFMAs to save registers)
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (i < 12) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-  };
-
-  // One pipeline step for tile t of this wave: softmax of S_t (already in
-  // s_cur), O^T += V^T . P^T from V buffer vb, and S_{t+1} = K . Q^T from K
-  // buffer kb_next into s_next.  The S_{t+1} MFMAs are issued between the
-  // exponentials of tile t, so the matrix and vector pipes work on different
-  // tiles at the same time.  `loads` issues the step's global loads after the
-  // exponentials, where S_t is dead and the registers they fill are free;
-  // every wave issues them, since the whole workgroup stages each tile.
-  auto step = [&](int t, bool run, f32x16 (&s_cur)[2], f32x16 (&s_next)[2], const uint16_t* kb_next,
-                  const uint16_t* vb, auto&& loads) {
+  // Causal / length mask of tile t in registers (only tiles that cross the
+  // diagonal or the end of the keys, and tiles past the window, which are
+  // wholly masked): key kv0 + 4h + off is visible iff off < rem.
+  auto mask_tile = [&](int t, int t_end, f32x16 (&s)[2]) {
     const int kv0 = t * kBN;
-    // not run, or tile t (and every later one) above this wave's diagonal:
-    // nothing but the loads
-    const bool active = run && kv0 <= c + m0w + 31;
-    bf16x8 pop[4];
-    if (active) {
-    if ((kv0 + kBN - 1 > c + m0w) || (kv0 + kBN > Lk)) {
-      // key kv0 + 4h + off is visible iff off < rem (keys up to c + tq, below Lk)
-      const int rem = min(c + tq + 1, Lk) - kv0 - 4 * h;
+    if ((kv0 + kBN - 1 > c + m0w) || (kv0 + kBN > Lk) || t >= t_end) {
+      const int rem = (t >= t_end) ? 0 : min(c + tq + 1, Lk) - kv0 - 4 * h;
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int off = 32 * rb + (i & 3) + 8 * (i >> 2);
-          s_cur[rb][i] = (off < rem) ? s_cur[rb][i] : -INFINITY;
+          s[rb][i] = (off < rem) ? s[rb][i] : -INFINITY;
         }
     }
-    // The maximum is taken over raw scores (scale > 0); exponents are
-    // exp2(s * scale_log2 - m) with m in log2 units.
-    float mx = -INFINITY;
+  };
+  // Row maximum of tile s in pieces: elements 8q..8q+7, then the running
+  // maximum is moved from the maximum of the pieces (raw scores; the scale
+  // is positive): the lanes whose maximum exceeds the reference by more than
+  // kLazyRescaleLog2 move it (lazy rescale).  The update scales the row sum
+  // and returns whether any lane moved; alpha is the factor for the
+  // accumulators.
+  auto max8 = [&](const f32x16 (&s)[2], int q) {
+    const int rb = q >> 1, o = 8 * (q & 1);
+    float m = fmaxf(s[rb][o], s[rb][o + 1]);
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s_cur[rb][i]);
+    for (int j = 2; j < 8; ++j) m = fmaxf(m, s[rb][o + j]);
+    return m;
+  };
+  auto update_max_from = [&](float mx, float& alpha) {
     {  // the other half of the column (lane l ^ 32) through v_permlane32_swap, no LDS round trip
       const uint32_t u = __builtin_bit_cast(uint32_t, mx);
       const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
       const uint32_t s0 = sw[0], s1 = sw[1];
       mx = fmaxf(__builtin_bit_cast(float, s0), __builtin_bit_cast(float, s1)) * p.scale_log2;
     }
-    const bool grow = mx > m_run + kLazyRescaleLog2;  // lazy rescale (see kLazyRescaleLog2)
-    if (wave_any(grow)) {
-      const float m_new = grow ? mx : m_run;
-      const float alpha = grow ? fast_exp2(m_run - m_new) : 1.f;
-      m_run = m_new;
-      l_run *= alpha;
+    const bool grow = mx > m_run + kLazyRescaleLog2;
+    alpha = grow ? fast_exp2(m_run - mx) : 1.f;
+    m_run = grow ? mx : m_run;
+    m_use = (m_run == -INFINITY) ? 0.f : m_run;
+    l_run *= alpha;
+    return wave_any(grow);
+  };
+  auto update_max = [&](const f32x16 (&s)[2], float& alpha) {
+    return update_max_from(fmaxf(fmaxf(max8(s, 0), max8(s, 1)), fmaxf(max8(s, 2), max8(s, 3))), alpha);
+  };
+  auto rescale_acc = [&](float alpha) {
 #pragma unroll
-      for (int db = 0; db < 4; ++db) acc[db] *= alpha;
-    }
-    const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
+    for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+  };
 
-    // exponentials of tile t, two behind each S_{t+1} MFMA: element n of
-    // S_t is s_cur[n / 16][n % 16]; word i of the P^T operands holds
-    // elements 2i and 2i + 1.  The row sum adds the bf16 weights the PV
-    // MFMAs use, two per v_dot2_f32_bf16 (against 1.0, 1.0).
-    uint32_t pw[16];
-    float ps = 0.f;
-    qk_mfma(kb_next, s_next, [&](int i) {
-      const int rb = i >> 3, n = (2 * i) & 15;
-      const float e0 = fast_exp2(__builtin_fmaf(s_cur[rb][n], p.scale_log2, -m_use));
-      const float e1 = fast_exp2(__builtin_fmaf(s_cur[rb][n + 1], p.scale_log2, -m_use));
-      pw[i] = pack_bf16x2(e0, e1);
-      ps = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[i]), __builtin_bit_cast(bf16x2, 0x3f803f80u),
-                                           ps, false);
-    });
-    l_run += ps;
+  // ---- the two halves of a pipeline step --------------------------------------
+  // Step t of a wave (tile t visible to it): part A computes S_{t+1} = K_{t+1}
+  // Q^T from K buffer kb with the exponentials of S_t's words 4..15 between
+  // its MFMAs; part B computes O^T += V_t^T P_t^T from V buffer vb with, between
+  // its MFMAs, the row maximum of S_{t+1}, the step's global loads, the staging
+  // of the tiles loaded one step earlier and the exponentials of S_{t+1}'s
+  // words 0..3.  Every MFMA of the step thus has a share of the vector work
+  // behind it.  Operands are read from LDS four MFMAs ahead.
+  auto vaddr = [&](const uint16_t* vb, int i) {  // V^T operand of PV MFMA i (k-step i/4, dim block i%4)
+    const int ks = i >> 2, d = 32 * (i & 3) + col;
+    return vb + d * kVPitch + ((16 * ks + 8 * h) ^ v_swz(d));
+  };
+  // Part A also reads part B's first four V^T operands (from vb) behind its
+  // last MFMAs.
+  auto part_a = [&](const uint16_t* kb, const uint16_t* vb, const f32x16 (&s_cur)[2], f32x16 (&s_next)[2],
+                    uint32_t (&pw)[16], u32x4 (&vpre)[kLead]) {
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) pop[ks] = as_bf16x8(pw[4 * ks], pw[4 * ks + 1], pw[4 * ks + 2], pw[4 * ks + 3]);
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s_next[rb][i] = 0.f;
+    const uint16_t* kr = kb + col * kKPitch + 8 * h;
+    auto kaddr = [&](int i) { return kr + (i & 1) * 32 * kKPitch + 16 * (i >> 1); };
+    u32x4 pre[kLead];
+#pragma unroll
+    for (int i = 0; i < kLead; ++i) pre[i] = *reinterpret_cast<const u32x4*>(kaddr(i));
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const u32x4 cur = pre[i % kLead];
+      if (i + kLead < 16) pre[i % kLead] = *reinterpret_cast<const u32x4*>(kaddr(i + kLead));
+      else vpre[i + kLead - 16] = *reinterpret_cast<const u32x4*>(vaddr(vb, i + kLead - 16));
+      s_next[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(cur), qop[i >> 1], s_next[i & 1], 0, 0, 0);
+      if (i < 12) exp_pair(s_cur, 4 + i, pw, ps_pend);
+    }
+    // the first exponentials run while the first K operands are in flight
+    __builtin_amdgcn_sched_group_barrier(0x100, kLead, 0);
+    __builtin_amdgcn_sched_group_barrier(0x402, 6, 0);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (i < 12) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x402, 7, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (i < 11) __builtin_amdgcn_sched_group_barrier(0x402, 6, 0);
     }
+    l_run += ps_pend;
+#pragma unroll
+    for (int i = 4; i < 16; ++i) pin(pw[i]);
+#pragma unroll
+    for (int i = 0; i < kLead; ++i) pin(vpre[i]);
+    pin(l_run);
+  };
+
+  // Part B places its work by hand, one segment per MFMA (sched_barrier
+  // fences): the loads, the row maximum of S_{t+1} in four pieces, its
+  // exchange and the running-maximum update, the staging in four quarters,
+  // and S_{t+1}'s words 0..3, one per segment.
+  auto part_b = [&](const uint16_t* vb, u32x4 (&vpre)[kLead], const uint32_t (&pw)[16], const f32x16 (&s_next)[2],
+                    uint32_t (&pw_next)[16], float& alpha, bool& any_grow, auto&& loads, auto&& stage_quarter) {
+    bf16x8 pop[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) pop[ks] = as_bf16x8(pw[4 * ks], pw[4 * ks + 1], pw[4 * ks + 2], pw[4 * ks + 3]);
+    float mq[4];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const u32x4 cur = vpre[i % kLead];
+      if (i + kLead < 16) vpre[i % kLead] = *reinterpret_cast<const u32x4*>(vaddr(vb, i + kLead));
+      acc[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(cur), pop[i >> 2], acc[i & 3], 0, 0, 0);
+      if (i == 0) loads();
+      if (i >= 2 && i < 6) mq[i - 2] = max8(s_next, i - 2);
+      if (i == 6) any_grow = update_max_from(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3])), alpha);
+      if (i == 7) stage_quarter(std::integral_constant<int, 0>{});
+      if (i == 8) stage_quarter(std::integral_constant<int, 1>{});
+      if (i == 9) stage_quarter(std::integral_constant<int, 2>{});
+      if (i == 10) stage_quarter(std::integral_constant<int, 3>{});
+      if (i == 11) ps_pend = 0.f;
+      if (i >= 11 && i < 15) exp_pair(s_next, i - 11, pw_next, ps_pend);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_sched_barrier(0);
-    loads();
-    __builtin_amdgcn_sched_barrier(0);
-    if (active) pv(pop, vb);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pin(pw_next[j]);
+    pin(ps_pend);
+    pin(l_run);
+    pin(m_use);
   };
 
   // ---- tile loop, one block-table window at a time -----------------------------
@@ -420,48 +460,107 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
   uint16_t* kbuf1 = lds + kKElems;
   uint16_t* vbuf0 = lds + 2 * kKElems;
   uint16_t* vbuf1 = vbuf0 + kVElems;
-  const int win_tiles = paged ? kBtWindow * p.block_size / kBN : n_tiles;
+  const int win_tiles = PAGED ? kBtWindow * p.block_size / kBN : n_tiles;
+  // The tile loop, specialised for the wave's role (K or V staging).
+  auto tile_loop = [&](auto role) {
   for (int t0 = 0; t0 < n_tiles; t0 += win_tiles) {
     const int t1 = min(n_tiles, t0 + win_tiles);
-    if (paged) {
+    if constexpr (PAGED) {
       win_base = (t0 * kBN) / p.block_size;
       const int bi = min(win_base + lane, (int)p.bt_stride - 1);
       bt_lane = p.block_tables[(int64_t)seq * p.bt_stride + bi];
     }
     auto in_win = [&](int t) { return t < t1 ? t : n_tiles; };
     TileRegs ra, rb;
-    load(t0, t0, ra);
-    if (k_role) {
-      load(in_win(t0 + 1), 0, rb);
+    load(role, t0, t0, ra);
+    if constexpr (decltype(role)::value) {
+      load(role, in_win(t0 + 1), 0, rb);
       stage_k(ra, kbuf0);
       stage_k(rb, kbuf1);
     } else {
       stage_v(ra, vbuf0);
     }
-    load(in_win(t0 + 2), in_win(t0 + 1), ra);
+    load(role, in_win(t0 + 2), in_win(t0 + 1), ra);
     wait_lds();
     __syncthreads();
+    // Prologue: S_{t0}, its maximum and the exponentials of its words 0..3.
     f32x16 sa[2], sb[2];
-    qk_mfma(kbuf0, sa, [](int) {});
-    for (int t = t0; t < t1; t += 2) {
-      step(t, true, sa, sb, kbuf1, vbuf0, [&] { load(in_win(t + 3), in_win(t + 2), rb); });
-      if (k_role) stage_k(ra, kbuf0);
-      else stage_v(ra, vbuf1);
+    uint32_t pa[16], pb[16];
+    {
+#pragma unroll
+      for (int rb_ = 0; rb_ < 2; ++rb_)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sa[rb_][i] = 0.f;
+      const uint16_t* kr = kbuf0 + col * kKPitch + 8 * h;
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        sa[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            as_bf16x8(*reinterpret_cast<const u32x4*>(kr + (i & 1) * 32 * kKPitch + 16 * (i >> 1))), qop[i >> 1],
+            sa[i & 1], 0, 0, 0);
+      mask_tile(t0, t1, sa);
+      float alpha;
+      if (update_max(sa, alpha)) rescale_acc(alpha);
+      ps_pend = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) exp_pair(sa, j, pa, ps_pend);
+    }
+    // K buffer 0 is restaged during the first step: every wave's reads of it
+    // above must be done first.
+    __syncthreads();
+
+    // A step of tile t visible to this wave, and a step of a tile past it
+    // (tiles above the wave's diagonal, and past the window, whose steps only
+    // load and stage for the other waves).  Visibility is monotone in t, so
+    // the visible steps run first; each step ends with the one barrier.
+    auto full_step = [&](int t, f32x16 (&s_cur)[2], f32x16 (&s_next)[2], uint32_t (&pw)[16], uint32_t (&pw_next)[16],
+                         const uint16_t* kb_next, const uint16_t* vb, TileRegs& stage_regs, uint16_t* stage_kb,
+                         uint16_t* stage_vb, TileRegs& load_regs) {
+      u32x4 vpre[kLead];
+      part_a(kb_next, vb, s_cur, s_next, pw, vpre);
+      mask_tile(t + 1, t1, s_next);
+      float alpha = 1.f;
+      bool any_grow = false;
+      part_b(vb, vpre, pw, s_next, pw_next, alpha, any_grow, [&] { load(role, in_win(t + 3), in_win(t + 2), load_regs); },
+             [&](auto qc) { stage_q(role, stage_regs, stage_kb, stage_vb, qc); });
+      if (any_grow) rescale_acc(alpha);
       wait_lds();
       __syncthreads();
-      // past the window's last tile: no step, but the loads keep the same
-      // count in flight at the loop head
-      step(t + 1, t + 1 < t1, sb, sa, kbuf0, vbuf1, [&] { load(in_win(t + 4), in_win(t + 3), ra); });
-      if (k_role) stage_k(rb, kbuf1);
-      else stage_v(rb, vbuf0);
+    };
+    auto idle_step = [&](int t, TileRegs& stage_regs, uint16_t* stage_kb, uint16_t* stage_vb, TileRegs& load_regs) {
+      load(role, in_win(t + 3), in_win(t + 2), load_regs);
+      stage(role, stage_regs, stage_kb, stage_vb);
       wait_lds();
       __syncthreads();
+    };
+    // Steps at an even offset from t0 compute S into sb from K buffer 1, read V
+    // buffer 0, stage ra into K buffer 0 / V buffer 1 and load into rb; odd
+    // steps swap every pair.
+    const int t_vis = max(t0, min(t1, (c + m0w + 31) / kBN + 1));
+    int t = t0;
+    for (; t + 1 < t_vis; t += 2) {
+      full_step(t, sa, sb, pa, pb, kbuf1, vbuf0, ra, kbuf0, vbuf1, rb);
+      full_step(t + 1, sb, sa, pb, pa, kbuf0, vbuf1, rb, kbuf1, vbuf0, ra);
+    }
+    if (t < t_vis) {
+      full_step(t, sa, sb, pa, pb, kbuf1, vbuf0, ra, kbuf0, vbuf1, rb);
+      ++t;
+      if (t < t1) {
+        idle_step(t, rb, kbuf1, vbuf0, ra);
+        ++t;
+      }
+    }
+    for (; t < t1; t += 2) {
+      idle_step(t, ra, kbuf0, vbuf1, rb);
+      if (t + 1 < t1) idle_step(t + 1, rb, kbuf1, vbuf0, ra);
     }
   }
+  };
+  if (k_role) tile_loop(std::true_type{});
+  else tile_loop(std::false_type{});
 
   // ---- normalise and store ----------------------------------------------------
   l_run += shfl_xor_f32(l_run, 32);
-  const int64_t row = (int64_t)geo.q_start + tq;
+  const int64_t row = (int64_t)q_start + tq;
   if (tq < Lq && row < p.q_rows) {
     const float inv = (l_run > 0.f) ? 1.0f / l_run : 0.f;
     uint16_t* op = p.out + (row * p.Hq + head) * kHeadDim;
@@ -479,8 +578,10 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
   }
 }
 
+static_assert(sizeof(PrefillItem) == 32, "the host sizes the work list with 32-byte records");
+
 int64_t prefill_schedule_bytes(const PrefillParams& p) {
-  return (int64_t)p.num_seqs * p.n_mblocks * (int64_t)sizeof(int2);
+  return (int64_t)p.num_seqs * p.n_mblocks * (int64_t)sizeof(PrefillItem);
 }
 
 hipError_t launch_varlen_prefill(const PrefillParams& p, const void* schedule, const MqParams& mq, bool merge,
@@ -490,8 +591,12 @@ hipError_t launch_varlen_prefill(const PrefillParams& p, const void* schedule, c
   const int64_t n_blocks = n_items_max * p.Hkv * p.n_hgroups;
   const int64_t n_merge = merge ? mq.num_seqs : 0;
   if (n_blocks + n_merge > 0x7fffffff || schedule == nullptr) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(varlen_prefill_kernel, dim3((unsigned)(n_blocks + n_merge)), dim3(64 * kPrefillWaves), 0, stream,
-                     p, static_cast<const int2*>(schedule), mq, (int)n_blocks);
+  const dim3 grid((unsigned)(n_blocks + n_merge)), block(64 * kPrefillWaves);
+  const PrefillItem* items = static_cast<const PrefillItem*>(schedule);
+  if (p.block_tables != nullptr)
+    hipLaunchKernelGGL(varlen_prefill_kernel<true>, grid, block, 0, stream, p, items, mq, (int)n_blocks);
+  else
+    hipLaunchKernelGGL(varlen_prefill_kernel<false>, grid, block, 0, stream, p, items, mq, (int)n_blocks);
   return hipGetLastError();
 }
 
