@@ -17,6 +17,9 @@ Secondary fields in the same JSON line:
                unmasked causal pairs, vs the bf16 dense MFMA peak;
   long_decode  long-context decode at Qwen3-32B shapes (64/8 heads, B = 32,
                context U[32K, 128K], 1% of K/V x20).
+Both are timed after 0.15 s of sustained warm-up calls (the shader clock
+settles lower under continuous MFMA load within the first tens of
+milliseconds); the headline decode field runs exactly --warmup warm-up calls.
 
 Inputs are resident in HBM before timing; two KV pools with different
 contents are alternated so the working set stays far above the 256 MB
@@ -60,6 +63,11 @@ SCALE = 128 ** -0.5
 METRIC = "decode attn HBM GB/s (%peak) + prefill attn TFLOP/s, Qwen3-8B shapes, FP8 KV"
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "decode_qwen3_0p6b_b256_pmc.json")
 COPY_PROBE_BYTES = 1 << 30
+# The secondary fields (prefill, long decode) are timed after this much
+# sustained warm-up: under continuous MFMA load the shader clock drops over
+# the first tens of milliseconds, and the steady state is what a serving
+# loop sees.  The headline decode field keeps exactly --warmup warm-up calls.
+SECONDARY_WARM_S = 0.15
 
 
 def parse():
@@ -78,11 +86,22 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def timed(fn, steps, warmup):
+def timed(fn, steps, warmup, warm_s=0.0):
     """Average ms per call over `steps` back-to-back calls, HIP events on the
-    current stream (the stream the kernels are launched on)."""
+    current stream (the stream the kernels are launched on).  `warmup` calls
+    run first; with warm_s > 0, warm-up calls continue until that many seconds
+    of them have run (the shader clock settles under sustained load)."""
     for i in range(warmup):
         fn(i)
+    if warm_s > 0:
+        torch.cuda.synchronize()
+        t_end = time.perf_counter() + warm_s
+        i = warmup
+        while time.perf_counter() < t_end:
+            for _ in range(8):
+                fn(i)
+                i += 1
+            torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -106,7 +125,7 @@ def gpu_pools(wl, n_pools):
     return pools
 
 
-def bench_decode(wl, steps, warmup, n_pools=2):
+def bench_decode(wl, steps, warmup, n_pools=2, warm_s=0.0):
     pools = gpu_pools(wl, n_pools)
     q = wl.make_q("cuda")
     bt = torch.from_numpy(wl.block_tables).cuda()
@@ -116,12 +135,12 @@ def bench_decode(wl, steps, warmup, n_pools=2):
         kc, vc = pools[i % n_pools]
         fp8_decode_attention(q, kc, vc, bt, ctx, SCALE)
 
-    ms = timed(step, steps, warmup)
+    ms = timed(step, steps, warmup, warm_s)
     nbytes = wl.decode_bytes()
     return dict(ms=ms, bytes=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9), pools, q
 
 
-def bench_prefill(wl, steps, warmup, n_pools=2):
+def bench_prefill(wl, steps, warmup, n_pools=2, warm_s=0.0):
     pools = gpu_pools(wl, n_pools)
     q = wl.make_q("cuda")
     bt = torch.from_numpy(wl.block_tables).cuda()
@@ -133,7 +152,7 @@ def bench_prefill(wl, steps, warmup, n_pools=2):
         fp8_prefill_attention(q, kc, vc, block_tables=bt, cu_seqlens_q=cu_q, cu_seqlens_k=cu_k,
                               max_seqlen_q=max_q, max_seqlen_k=max_k, softmax_scale=SCALE)
 
-    ms = timed(step, steps, warmup)
+    ms = timed(step, steps, warmup, warm_s)
     flops = wl.attention_flops()
     return dict(ms=ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12), pools, q
 
@@ -234,7 +253,7 @@ def main():
     if args.only in ("prefill", "all"):
         wl = W.qwen3_8b_prefill()
         log(f"prefill workload {wl.name}: flops={wl.attention_flops()}")
-        res, pools, _ = bench_prefill(wl, max(args.steps // 2, 5), max(args.warmup // 2, 2))
+        res, pools, _ = bench_prefill(wl, max(args.steps // 2, 5), max(args.warmup // 2, 2), warm_s=SECONDARY_WARM_S)
         log(f"prefill: {res['ms'] * 1e3:.1f} us/step, {res['tflops']:.1f} TFLOP/s")
         extra["prefill"] = dict(workload=wl.name, ms_per_step=round(res["ms"], 5),
                                 tflops=round(res["tflops"], 2),
@@ -247,7 +266,8 @@ def main():
     if args.only in ("long", "all"):
         wl = W.qwen3_32b_long_decode()
         log(f"long decode workload {wl.name}: bytes={wl.decode_bytes()}")
-        res, pools, _ = bench_decode(wl, max(args.steps // 5, 5), max(args.warmup // 5, 2), n_pools=1)
+        res, pools, _ = bench_decode(wl, max(args.steps // 5, 5), max(args.warmup // 5, 2), n_pools=1,
+                                     warm_s=SECONDARY_WARM_S)
         log(f"long decode: {res['ms'] * 1e3:.1f} us/step, {res['gbs']:.1f} GB/s")
         extra["long_decode"] = dict(workload=wl.name, ms_per_step=round(res["ms"], 5),
                                     gbs=round(res["gbs"], 2), frac_hbm_peak=round(res["gbs"] / HBM_PEAK_GBS, 4),
