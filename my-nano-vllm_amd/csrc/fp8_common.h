@@ -16,6 +16,8 @@ namespace nvamd {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -46,6 +48,15 @@ __device__ __forceinline__ u32x2 fp8x4_to_bf16x4(uint32_t w) {
   return r;
 }
 
+// Four E4M3FN bytes -> fp16 x4 as two dwords.  Exact: every E4M3FN value
+// (|x| <= 448, subnormals down to 2^-9) is an fp16 value.
+__device__ __forceinline__ u32x2 fp8x4_to_f16x4(uint32_t w) {
+  u32x2 r;
+  r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false));
+  r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true));
+  return r;
+}
+
 // Saturating clamp applied before the hardware RNE conversion: |x| > 448
 // (including inf) -> +-448; NaN passes through unchanged.
 __device__ __forceinline__ float e4m3_satfinite(float x) {
@@ -69,6 +80,19 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   f32x2 v = {lo, hi};
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
+
+// Two fp32 -> two fp16 (round to nearest even) in one dword: v_cvt_pk_f16_f32.
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+}
+
+__device__ __forceinline__ f16x8 as_f16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  u32x4 t = {a, b, c, d};
+  return __builtin_bit_cast(f16x8, t);
+}
+
+__device__ __forceinline__ f16x8 as_f16x8(u32x4 t) { return __builtin_bit_cast(f16x8, t); }
 
 // 2**x with the bare v_exp_f32 (inputs here are <= 0 or -inf; tiny results
 // may flush to zero, which is harmless for softmax weights).

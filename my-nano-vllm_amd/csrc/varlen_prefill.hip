@@ -19,29 +19,32 @@
 //
 // K/V stream in 64-token tiles, K one tile ahead of V.  Waves 0..3 load and
 // stage K tiles, waves 4..7 V tiles: each thread loads its share of an FP8
-// tile into registers two steps ahead (bounded raw buffer loads: rows past
-// the sequence read as zero, so every iteration issues the same loads and
-// the compiler's wait counts stay exact), converts it to bf16 (exact) and
-// stages it in one of two LDS buffers -- K as [token][dim], V transposed as
-// [dim][token] -- while the waves compute the other buffer.  One barrier
-// per tile.  Each K load instruction fetches 8 rows (8 lanes per row), each
-// V load instruction 4 whole rows.
+// tile into registers a step ahead (bounded raw buffer loads: rows past the
+// sequence read as zero, so every iteration issues the same loads and the
+// compiler's wait counts stay exact), converts it exactly -- K to bf16, V to
+// fp16 -- and stages it in one of two LDS buffers, K as [token][dim], V
+// transposed as [dim][token].  One barrier per tile.  Each K load
+// instruction fetches 8 rows (8 lanes per row), each V load instruction 4
+// whole rows.
 //
-// Per tile a wave computes with v_mfma_f32_32x32x16_bf16 (fp32 accumulate):
-//     S^T[kv][q] = K[kv][:] . Q[q][:]          2 row blocks x 8 k-steps
-//     O^T[d][q] += V^T[d][kv] . P^T[kv][q]     4 dim blocks x 4 k-steps
-// Lane l (h = l / 32) holds query column l % 32; in the S^T result it holds
-// kv tokens (i%4) + 8(i/4) + 4h of each 32-token row block, so the PV
-// operand for k-step ks is simply p[ks/2][8(ks%2) .. +8) once V^T is stored
-// with bits 2 and 3 of the token index swapped inside each 16-token step.
-// The V^T rows XOR their 16-byte chunks with bits 5..6 of the dim index and
-// the V staging lanes are arranged so the transposing stores, the K stores
-// and the MFMA operand reads are all free of LDS bank conflicts.  The causal
-// mask is applied in registers only on tiles that cross the diagonal (or
-// the end of the sequence); tiles wholly above a wave's rows are skipped.
-// Step t of a wave runs the softmax of S_t with the MFMAs of S_{t+1}
-// interleaved between its exponentials, then O += P_t V_t.  The kernel is
-// register-budgeted for two waves per SIMD (one workgroup per CU).
+// Per tile a wave computes (fp32 accumulate)
+//     S^T[kv][q] = K[kv][:] . Q[q][:]          v_mfma_f32_32x32x16_bf16, 2 row blocks x 8 k-steps
+//     O^T[d][q] += V^T[d][kv] . P^T[kv][q]     v_mfma_f32_32x32x16_f16,  4 dim blocks x 4 k-steps
+// The softmax weights P are rounded to fp16 (11-bit significand; the lazy
+// rescale keeps them <= 2^8), V is exact in fp16.  Lane l (h = l / 32) holds
+// query column l % 32; in the S^T result it holds kv tokens (i%4) + 8(i/4) +
+// 4h of each 32-token row block, so the PV operand for k-step ks is simply
+// p[ks/2][8(ks%2) .. +8) once V^T is stored with bits 2 and 3 of the token
+// index swapped inside each 16-token step.  The V^T rows XOR their 16-byte
+// chunks with bits 5..6 of the dim index and the V staging lanes are
+// arranged so the transposing stores, the K stores and the MFMA operand
+// reads are all free of LDS bank conflicts.  The causal mask is applied in
+// registers only on tiles that cross the diagonal (or the end of the
+// sequence); tiles wholly above a wave's rows only load and stage.  Step t
+// of a wave is two stretches of 16 MFMAs with the vector work spread
+// between them (part A: S_{t+1} and most of S_t's exponentials; part B:
+// O += P_t V_t, S_{t+1}'s maximum, the loads and the staging).  The kernel
+// is register-budgeted for two waves per SIMD (one workgroup per CU).
 #include <type_traits>
 
 #include "fp8_common.h"
@@ -55,10 +58,10 @@ namespace {
 
 constexpr int kBN = kPrefillTile;             // kv tokens per tile
 constexpr int kKPitch = kHeadDim + 8;         // bf16 per K row in LDS (272 B)
-constexpr int kVPitch = kBN + 8;              // bf16 per V^T row in LDS (144 B)
+constexpr int kVPitch = kBN + 8;              // fp16 per V^T row in LDS (144 B)
 constexpr int kKElems = kBN * kKPitch;        // 8704
 constexpr int kVElems = kHeadDim * kVPitch;   // 9216
-constexpr int kBufElems = kKElems + kVElems;  // 17920 bf16 = 35840 B per K + V pair
+constexpr int kBufElems = kKElems + kVElems;  // 17920 16-bit = 35840 B per K + V pair
 constexpr int kBtWindow = 64;                 // block-table entries held in one register
 constexpr int kLead = 4;                      // MFMA operands are read from LDS this many MFMAs ahead
 
@@ -77,7 +80,7 @@ __device__ __forceinline__ int v_pos(int t) {
   return (t & ~12) | (b2 << 3) | (b3 << 2);
 }
 
-// Chunk swizzle of V^T row `dim`: XOR of the column (in bf16) with 16 *
+// Chunk swizzle of V^T row `dim`: XOR of the column (in 16-bit elements) with 16 *
 // bits 5..6 of the dim.  It is constant across the 32 rows one MFMA operand
 // read touches (those rows are conflict-free as they are: 144-byte pitch),
 // and separates the dim blocks a staging store group writes.  Keeps 8-element
@@ -259,7 +262,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
 #pragma unroll
     for (int i = 0; i < 4; ++i) stage_k_q(kr, kb, i);
   };
-  // Transposes a V tile share (4 tokens x 8 dims) to bf16 and writes it to
+  // Transposes a V tile share (4 tokens x 8 dims) to fp16 and writes it to
   // V^T buffer vb: one 8-byte store (4 tokens) per dim, in four quarters of
   // two dims each.  Dims v_byte..v_byte+7 share one chunk swizzle (v_byte is
   // a multiple of 8), so the 8 stores are one address plus constant offsets.
@@ -280,8 +283,8 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
     const uint32_t t0 = __builtin_amdgcn_perm(x, y, 0x01000504u);  // [a_j b_j c_j d_j]
     const uint32_t t1 = __builtin_amdgcn_perm(x, y, 0x03020706u);  // [a_j+1 b_j+1 c_j+1 d_j+1]
     constexpr int kRow = 2 * kVPitch;  // bytes per V^T row
-    lds_store8<(2 * q) * kRow>(vd, fp8x4_to_bf16x4(t0));
-    lds_store8<(2 * q + 1) * kRow>(vd, fp8x4_to_bf16x4(t1));
+    lds_store8<(2 * q) * kRow>(vd, fp8x4_to_f16x4(t0));
+    lds_store8<(2 * q + 1) * kRow>(vd, fp8x4_to_f16x4(t1));
   };
   auto stage_v = [&](const TileRegs& vr, uint16_t* vb) {
     stage_v_q(vr, vb, std::integral_constant<int, 0>{});
@@ -303,15 +306,15 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
   // Element n of an S^T tile is s[n / 16][n % 16]; lane (h, col) holds kv
   // token 32*(n/16) + (n%4) + 8*((n%16)/4) + 4h of query column col.
   // Word i of the P^T operands holds the weights of elements 2i and 2i + 1;
-  // the row sum adds the bf16 weights the PV MFMAs use, two per
-  // v_dot2_f32_bf16 (against 1.0, 1.0).
-  const bf16x2 ones = __builtin_bit_cast(bf16x2, 0x3f803f80u);
+  // the row sum adds the fp16 weights the PV MFMAs use, two per
+  // v_dot2_f32_f16 (against 1.0, 1.0).
+  const f16x2 ones = __builtin_bit_cast(f16x2, 0x3c003c00u);
   auto exp_pair = [&](const f32x16 (&s)[2], int i, uint32_t (&pw)[16], float& ps) {
     const int rb = i >> 3, n = (2 * i) & 15;
     const float e0 = fast_exp2(__builtin_fmaf(s[rb][n], p.scale_log2, -m_use));
     const float e1 = fast_exp2(__builtin_fmaf(s[rb][n + 1], p.scale_log2, -m_use));
-    pw[i] = pack_bf16x2(e0, e1);
-    ps = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[i]), ones, ps, false);
+    pw[i] = pack_f16x2(e0, e1);
+    ps = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pw[i]), ones, ps, false);
   };
   // Causal / length mask of tile t in registers (only tiles that cross the
   // diagonal or the end of the keys, and tiles past the window, which are
@@ -420,15 +423,15 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
   // and S_{t+1}'s words 0..3, one per segment.
   auto part_b = [&](const uint16_t* vb, u32x4 (&vpre)[kLead], const uint32_t (&pw)[16], const f32x16 (&s_next)[2],
                     uint32_t (&pw_next)[16], float& alpha, bool& any_grow, auto&& loads, auto&& stage_quarter) {
-    bf16x8 pop[4];
+    f16x8 pop[4];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) pop[ks] = as_bf16x8(pw[4 * ks], pw[4 * ks + 1], pw[4 * ks + 2], pw[4 * ks + 3]);
+    for (int ks = 0; ks < 4; ++ks) pop[ks] = as_f16x8(pw[4 * ks], pw[4 * ks + 1], pw[4 * ks + 2], pw[4 * ks + 3]);
     float mq[4];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const u32x4 cur = vpre[i % kLead];
       if (i + kLead < 16) vpre[i % kLead] = *reinterpret_cast<const u32x4*>(vaddr(vb, i + kLead));
-      acc[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(cur), pop[i >> 2], acc[i & 3], 0, 0, 0);
+      acc[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(cur), pop[i >> 2], acc[i & 3], 0, 0, 0);
       if (i == 0) loads();
       if (i >= 2 && i < 6) mq[i - 2] = max8(s_next, i - 2);
       if (i == 6) any_grow = update_max_from(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3])), alpha);

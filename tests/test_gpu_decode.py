@@ -146,3 +146,36 @@ def test_decode_block_permutation_invariance():
     ctx = torch.from_numpy(wl.context_lens()).cuda()
     out2 = fp8_decode_attention(q, kc2, vc2, bt2, ctx, SCALE)
     assert torch.equal(out1, out2)
+
+
+def _forced_split_decode(wl, gpu_c, qg, part_tokens):
+    bt = torch.from_numpy(wl.block_tables).cuda()
+    ctx = torch.from_numpy(wl.context_lens()).cuda()
+    lib = _native.load()
+    B, Hq = qg.shape[0], wl.num_heads
+    nb = bt.shape[1]
+    ws_bytes = lib.nvamd_decode_workspace_bytes(B, Hq, wl.num_kv_heads, nb, wl.block_size, part_tokens)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
+    out = torch.empty_like(qg)
+    st = lib.nvamd_fp8_decode_attention(out.data_ptr(), qg.data_ptr(), gpu_c[0].data_ptr(), gpu_c[1].data_ptr(),
+                                        bt.data_ptr(), ctx.data_ptr(), B, Hq, wl.num_kv_heads, 128,
+                                        wl.num_blocks, wl.block_size, nb, SCALE, part_tokens, ws.data_ptr(), ws_bytes,
+                                        torch.cuda.current_stream().cuda_stream)
+    _native.check(st, "decode")
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("ctx_lo,ctx_hi", [(30, 500), (2000, 8000)])
+def test_decode_outlier_kv(ctx_lo, ctx_hi):
+    """Qwen3-32B head shapes with 1 % of the K/V entries scaled by 20 before
+    quantisation (the long-decode configuration's outliers): peaked scores
+    and large V values, through the balanced kernel and the split-KV kernel."""
+    wl = W.decode_workload(f"decode_outliers_{ctx_lo}", 24, 64, 8, ctx_lo, ctx_hi, seed=31,
+                           outlier_frac=0.01, outlier_scale=20.0)
+    announce(f"decode: outlier K/V (1% x20), ctx U[{ctx_lo}, {ctx_hi}]")
+    cpu_c, gpu_c = build_pair(wl)
+    q = wl.make_q("cpu")
+    want = _oracle_decode(wl, cpu_c, q)
+    assert_close(_run_decode(wl, gpu_c, q.cuda()), want, "balanced decode, outliers")
+    assert_close(_forced_split_decode(wl, gpu_c, q.cuda(), 256), want, "split-KV decode, outliers")

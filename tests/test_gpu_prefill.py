@@ -104,10 +104,42 @@ def test_prefill_lq1_equals_decode():
 
 @pytest.mark.parametrize("bs", [64, 192, 512])
 def test_prefill_block_sizes(bs):
-    """Block sizes other than 256: powers of two take the shift path of the
-    tile addressing, 192 the division path; chunks cross many block borders."""
+    """Block sizes other than 256 (the block of a tile comes from a multiply
+    with the reciprocal of the tiles per block; 192 is not a power of two);
+    chunks cross many block borders."""
     rng = np.random.default_rng(bs)
     seqs = [W.SeqSpec(lq=int(l), cached=int(rng.integers(0, 900))) for l in (300, 129, 64, 7, 512)]
     wl = W.make_workload(f"prefill_bs{bs}", 32, 8, seqs, seed=int(rng.integers(1 << 30)), block_size=bs)
     announce(f"prefill: block_size {bs}")
+    _check(wl)
+
+
+@pytest.mark.parametrize("bs,cached,lq", [(64, 4500, 300), (256, 16900, 200)])
+def test_prefill_multi_window_block_tables(bs, cached, lq):
+    """Sequences with more than 64 blocks: the kernel holds a 64-entry window
+    of the block table in one register and reloads it at the window edge
+    (4096 tokens at block size 64, 16384 at 256); the chunk straddles it."""
+    seqs = [W.SeqSpec(lq=lq, cached=cached), W.SeqSpec(lq=65, cached=4000), W.SeqSpec(lq=33, cached=100)]
+    wl = W.make_workload(f"prefill_windows_bs{bs}", 32, 8, seqs, seed=bs + 11, block_size=bs)
+    announce(f"prefill: block-table windows, block_size {bs}, Lk {cached + lq}")
+    _check(wl)
+
+
+def test_prefill_outlier_kv():
+    """1 % of the K/V entries scaled by 20 before quantisation (peaked scores,
+    values near the E4M3 range): the lazy rescale and the bf16 weights stay
+    within tolerance."""
+    seqs = [W.SeqSpec(lq=l, cached=c) for l, c in ((512, 1500), (129, 3000), (64, 0), (300, 700), (5, 2000))]
+    wl = W.make_workload("prefill_outliers", 32, 8, seqs, seed=21, outlier_frac=0.01, outlier_scale=20.0)
+    announce("prefill: outlier K/V (1% x20)")
+    _check(wl)
+
+
+def test_prefill_zero_length_sequences():
+    """Sequences that contribute no query rows (repeated cu_seqlens_q entries),
+    with and without cached keys, between ordinary ones."""
+    seqs = [W.SeqSpec(lq=0, cached=300), W.SeqSpec(lq=100, cached=50), W.SeqSpec(lq=0, cached=0),
+            W.SeqSpec(lq=70, cached=900), W.SeqSpec(lq=3, cached=40), W.SeqSpec(lq=0, cached=1000)]
+    wl = W.make_workload("prefill_zero_lq", 32, 8, seqs, seed=23)
+    announce("prefill: zero-length sequences in the batch")
     _check(wl)
