@@ -16,8 +16,15 @@ Secondary fields in the same JSON line:
                512-token chunks over cached context U[0, 4096]) in TFLOP/s of
                unmasked causal pairs, vs the bf16 dense MFMA peak;
   long_decode  long-context decode at Qwen3-32B shapes (64/8 heads, B = 32,
-               context U[32K, 128K], 1% of K/V x20).
-Both are timed after 0.15 s of sustained warm-up calls (the shader clock
+               context U[32K, 128K], 1% of K/V x20);
+  store        the KV store/quantise of the prefill workload's 8192 new
+               tokens (strided K/V views of a fused qkv tensor), GB/s;
+  mixed        the mixed batch's varlen call (32 speculative x 5 rows + 3 x
+               512-token chunks, Qwen3-8B shapes), TFLOP/s, and its
+               speculative rows alone, GB/s over their decode bytes;
+  contiguous_prefill  the mixed batch's 1024-token contiguous-layout prompt
+               (block_tables=None), TFLOP/s.
+These are timed after 0.15 s of sustained warm-up calls (the shader clock
 settles lower under continuous MFMA load within the first tens of
 milliseconds); the headline decode field runs exactly --warmup warm-up calls.
 
@@ -38,7 +45,7 @@ parity tests' checker) on the host cores for a bounded sample of the same
 workload.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--only decode|prefill|long|all] [--no-cpu-baseline]
+                    [--only decode|prefill|long|store|mixed|all] [--no-cpu-baseline]
                     [--copy-probe]
 """
 import argparse
@@ -63,7 +70,7 @@ SCALE = 128 ** -0.5
 METRIC = "decode attn HBM GB/s (%peak) + prefill attn TFLOP/s, Qwen3-8B shapes, FP8 KV"
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "decode_qwen3_0p6b_b256_pmc.json")
 COPY_PROBE_BYTES = 1 << 30
-# The secondary fields (prefill, long decode) are timed after this much
+# The secondary fields (prefill, store, mixed, long decode) are timed after this much
 # sustained warm-up: under continuous MFMA load the shader clock drops over
 # the first tens of milliseconds, and the steady state is what a serving
 # loop sees.  The headline decode field keeps exactly --warmup warm-up calls.
@@ -75,7 +82,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="all", choices=["decode", "prefill", "long", "all"])
+    ap.add_argument("--only", default="all", choices=["decode", "prefill", "long", "store", "mixed", "all"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 1 GiB device copy (counter scale for rocprofv3 --pmc)")
@@ -155,6 +162,49 @@ def bench_prefill(wl, steps, warmup, n_pools=2, warm_s=0.0):
     ms = timed(step, steps, warmup, warm_s)
     flops = wl.attention_flops()
     return dict(ms=ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12), pools, q
+
+
+def bench_store(wl, steps, warmup, n_src=6):
+    """KV store/quantise of the workload's new tokens (the prefill step's own
+    K/V): key/value are strided views of a fused qkv tensor, as in the model
+    (q, k, v = qkv.split(...)); n_src source tensors rotate so the reads come
+    from HBM.  Algorithmic bytes: bf16 K/V read + FP8 K/V written + slot ids."""
+    n = wl.num_q_tokens()
+    hq, hkv = wl.num_heads, wl.num_kv_heads
+    slots = torch.from_numpy(wl.new_token_slots()).cuda()
+    kc, vc = wl.empty_caches("cuda")
+    srcs = []
+    g = torch.Generator(device="cuda").manual_seed(wl.seed)
+    for _ in range(n_src):
+        qkv = torch.randn(n, (hq + 2 * hkv) * 128, generator=g, device="cuda").to(torch.bfloat16)
+        k = qkv[:, hq * 128:(hq + hkv) * 128].view(n, hkv, 128)
+        v = qkv[:, (hq + hkv) * 128:].view(n, hkv, 128)
+        srcs.append((k, v))
+
+    def step(i):
+        k, v = srcs[i % n_src]
+        store_kvcache(k, v, kc, vc, slots)
+
+    ms = timed(step, steps, warmup, SECONDARY_WARM_S)
+    nbytes = n * hkv * 128 * (2 * 2 + 2) + 4 * n
+    return dict(ms=ms, bytes=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9)
+
+
+def bench_contiguous(n_tok, hq, hkv, steps, warmup):
+    """One contiguous-layout prompt (block_tables=None): FP8 K/V [n, Hkv, 128]."""
+    g = torch.Generator(device="cuda").manual_seed(17)
+    q = torch.randn(n_tok, hq, 128, generator=g, device="cuda").to(torch.bfloat16)
+    k = torch.randn(n_tok, hkv, 128, generator=g, device="cuda").to(torch.bfloat16).to(torch.float8_e4m3fn)
+    v = torch.randn(n_tok, hkv, 128, generator=g, device="cuda").to(torch.bfloat16).to(torch.float8_e4m3fn)
+    cu = torch.tensor([0, n_tok], dtype=torch.int32, device="cuda")
+
+    def step(i):
+        fp8_prefill_attention(q, k, v, block_tables=None, cu_seqlens_q=cu, cu_seqlens_k=cu,
+                              max_seqlen_q=n_tok, max_seqlen_k=n_tok, softmax_scale=SCALE)
+
+    ms = timed(step, steps, warmup, SECONDARY_WARM_S)
+    flops = 4 * 128 * hq * (n_tok * (n_tok + 1) // 2)
+    return dict(ms=ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12)
 
 
 def copy_probe(reps=4):
@@ -261,6 +311,45 @@ def main():
                                 algorithmic_flops_per_step=res["flops"],
                                 kernels="prefill_short_kernel<2,2> (short-query rows, none here, and the work list) + varlen_prefill_kernel")
         del pools
+        torch.cuda.empty_cache()
+
+    if args.only in ("store", "all"):
+        wl = W.qwen3_8b_prefill()
+        res = bench_store(wl, max(args.steps, 20), max(args.warmup, 5))
+        log(f"store: {res['ms'] * 1e3:.1f} us/step, {res['gbs']:.1f} GB/s")
+        extra["store"] = dict(workload=wl.name + " new tokens (8192 x 8 kv heads, strided K/V views of qkv)",
+                              ms_per_step=round(res["ms"], 5), gbs=round(res["gbs"], 2),
+                              frac_hbm_peak=round(res["gbs"] / HBM_PEAK_GBS, 4), algorithmic_bytes_per_step=res["bytes"],
+                              kernels="kv_store_fp8_kernel")
+        torch.cuda.empty_cache()
+
+    if args.only in ("mixed", "all"):
+        full = W.qwen3_8b_mixed()
+        varlen = W.sub_workload(full, range(full.extra["split_pt"], full.num_seqs), name="qwen3_8b_mixed_varlen")
+        spec = W.sub_workload(full, range(full.extra["split_pt"], full.extra["split_pt"] + full.extra["num_spec_seqs"]),
+                              name="qwen3_8b_mixed_spec")
+        res, pools, _ = bench_prefill(varlen, max(args.steps // 2, 5), max(args.warmup // 2, 2), warm_s=SECONDARY_WARM_S)
+        del pools
+        res_s, pools, _ = bench_prefill(spec, max(args.steps // 2, 5), max(args.warmup // 2, 2), warm_s=SECONDARY_WARM_S)
+        del pools
+        spec_bytes = spec.decode_bytes()
+        res_c = bench_contiguous(full.extra["contiguous_prompt_len"], full.num_heads, full.num_kv_heads,
+                                 max(args.steps // 2, 5), max(args.warmup // 2, 2))
+        log(f"mixed varlen: {res['ms'] * 1e3:.1f} us/step; spec rows: {res_s['ms'] * 1e3:.1f} us/step; "
+            f"contiguous prompt: {res_c['ms'] * 1e3:.1f} us/step")
+        extra["mixed"] = dict(
+            workload="qwen3_8b_mixed varlen call: 32 speculative x 5 rows + 3 x 512-token chunks (32/8 heads)",
+            ms_per_step=round(res["ms"], 5), tflops=round(res["tflops"], 2),
+            frac_bf16_peak=round(res["tflops"] / BF16_PEAK_TFLOPS, 4), algorithmic_flops_per_step=res["flops"],
+            spec_rows_only=dict(ms_per_step=round(res_s["ms"], 5), algorithmic_bytes_per_step=spec_bytes,
+                                gbs=round(spec_bytes / (res_s["ms"] * 1e-3) / 1e9, 2),
+                                frac_hbm_peak=round(spec_bytes / (res_s["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)),
+            kernels="prefill_short_kernel (speculative rows, split-KV) + varlen_prefill_kernel (chunks, and the merge)")
+        extra["contiguous_prefill"] = dict(
+            workload="qwen3_8b_mixed contiguous prompt: 1024 tokens, block_tables=None (32/8 heads)",
+            ms_per_step=round(res_c["ms"], 5), tflops=round(res_c["tflops"], 2),
+            frac_bf16_peak=round(res_c["tflops"] / BF16_PEAK_TFLOPS, 4), algorithmic_flops_per_step=res_c["flops"],
+            kernels="varlen_prefill_kernel<false>")
         torch.cuda.empty_cache()
 
     if args.only in ("long", "all"):

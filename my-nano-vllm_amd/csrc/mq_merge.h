@@ -17,6 +17,12 @@ __device__ __forceinline__ int key_capacity(const MqParams& p) {
 }
 
 // Log-sum-exp merge of the partitions of one (query row, head) by one wave.
+// Lane l of a 64-partition chunk holds partition l's (m, l) and its weight;
+// each lane holds two output dims.  The partial accumulators are loaded eight
+// partitions at a time, all issued before any is used (indices clamped to the
+// last partition, weights zero past it), so a merge of up to eight
+// partitions is one memory round trip after the (m, l) loads, not one per
+// partition.
 __device__ __forceinline__ void merge_partitions(const MqParams& p, int64_t rh, int Lk, int lane) {
   Lk = min(Lk, key_capacity(p));
   if (Lk <= 0) return;
@@ -24,41 +30,63 @@ __device__ __forceinline__ void merge_partitions(const MqParams& p, int64_t rh, 
   if (n_parts <= 1) return;
 
   const float* ml = p.part_ml + 2 * rh * p.max_parts;
+  const float* pa = p.part_acc + rh * p.max_parts * kHeadDim + 2 * lane;
   float M = -INFINITY;
-  for (int q = lane; q < n_parts; q += 64) M = fmaxf(M, ml[2 * q]);
+  for (int c = 0; c < n_parts; c += 64) {
+    const int qn = min(64, n_parts - c);
+    const float m = ml[2 * (c + min(lane, qn - 1))];
+    M = fmaxf(M, lane < qn ? m : -INFINITY);
+  }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, shfl_xor_f32(M, off));
   const float Ms = (M == -INFINITY) ? 0.f : M;
-  float L = 0.f;
-  for (int q = lane; q < n_parts; q += 64) L += ml[2 * q + 1] * fast_exp2(ml[2 * q] - Ms);
+
+  float L = 0.f, o0 = 0.f, o1 = 0.f;
+  for (int c = 0; c < n_parts; c += 64) {
+    const int qn = min(64, n_parts - c);
+    const f32x2 v = *reinterpret_cast<const f32x2*>(ml + 2 * (c + min(lane, qn - 1)));
+    const float w = (lane < qn) ? fast_exp2(v.x - Ms) : 0.f;
+    L += (lane < qn) ? v.y * w : 0.f;
+    for (int q0 = 0; q0 < qn; q0 += 8) {
+      f32x2 a[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        a[j] = *reinterpret_cast<const f32x2*>(pa + (int64_t)(c + min(q0 + j, qn - 1)) * kHeadDim);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float wj = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), min(q0 + j, 63)));
+        const float wk = (q0 + j < qn) ? wj : 0.f;
+        o0 += wk * a[j].x;
+        o1 += wk * a[j].y;
+      }
+    }
+  }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) L += shfl_xor_f32(L, off);
-
-  const float* pa = p.part_acc + rh * p.max_parts * kHeadDim + 2 * lane;
-  float o0 = 0.f, o1 = 0.f;
-  for (int q = 0; q < n_parts; ++q) {
-    const float w = fast_exp2(ml[2 * q] - Ms);
-    const f32x2 a = *reinterpret_cast<const f32x2*>(pa + (int64_t)q * kHeadDim);
-    o0 += w * a.x;
-    o1 += w * a.y;
-  }
   const float inv = (L > 0.f) ? 1.0f / L : 0.f;
   const uint32_t w = out_round_bf16_bits(o0 * inv) | (out_round_bf16_bits(o1 * inv) << 16);
   *reinterpret_cast<uint32_t*>(p.out + rh * kHeadDim + 2 * lane) = w;
 }
 
-// Varlen mode: the merges of sequence `seq` (only short-query sequences, the
-// ones the split-KV kernel served, have partitions), by `n_waves` waves.
-__device__ __forceinline__ void merge_varlen_seq(const MqParams& p, int seq, int wave, int n_waves, int lane) {
+// Varlen mode: merges of sequence `seq` (only short-query sequences, the
+// ones the split-KV kernel served, have partitions), one (row, head) per
+// wave: this wave merges index `idx` of the sequence's Lq * Hq (row, head)
+// pairs.  Launches give every pair a wave of its own, since a merge is a
+// chain of dependent memory round trips.
+__device__ __forceinline__ void merge_varlen_one(const MqParams& p, int seq, int idx, int lane) {
   const int row0 = p.cu_q[seq];
   const int Lq = p.cu_q[seq + 1] - row0;
-  if (Lq <= 0 || Lq > p.mq_max_q) return;
-  const int Lk = p.cu_k[seq + 1] - p.cu_k[seq];
-  for (int idx = wave; idx < Lq * p.Hq; idx += n_waves) {
-    const int64_t row = (int64_t)row0 + idx / p.Hq;
-    if (row >= p.q_rows) break;
-    merge_partitions(p, row * p.Hq + idx % p.Hq, Lk, lane);
-  }
+  if (Lq <= 0 || Lq > p.mq_max_q || idx >= Lq * p.Hq) return;
+  const int64_t row = (int64_t)row0 + idx / p.Hq;
+  if (row >= p.q_rows) return;
+  merge_partitions(p, row * p.Hq + idx % p.Hq, p.cu_k[seq + 1] - p.cu_k[seq], lane);
+}
+
+// Slices of `n_waves` (row, head) pairs per sequence: workgroups a varlen
+// merge launch needs per sequence.
+__host__ __device__ __forceinline__ int merge_slices(const MqParams& p, int n_waves) {
+  return (p.mq_max_q * p.Hq + n_waves - 1) / n_waves;
 }
 
 }  // namespace nvamd

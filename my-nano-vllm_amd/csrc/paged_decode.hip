@@ -586,9 +586,11 @@ __global__ __launch_bounds__(256) void mq_reduce_kernel(MqParams p) {
   merge_partitions(p, rh, p.context_lens[rh / p.Hq], lane);
 }
 
-// Varlen mode: one workgroup per sequence.
+// Varlen mode: workgroup (sequence, slice), one (row, head) per wave.
 __global__ __launch_bounds__(256) void mq_reduce_varlen_kernel(MqParams p) {
-  merge_varlen_seq(p, blockIdx.x, threadIdx.x >> 6, 4, threadIdx.x & 63);
+  const int slices = merge_slices(p, 4);
+  const int seq = (int)blockIdx.x / slices, slice = (int)blockIdx.x - seq * slices;
+  merge_varlen_one(p, seq, slice * 4 + (int)(threadIdx.x >> 6), threadIdx.x & 63);
 }
 
 // ---------------------------------------------------------------------------
@@ -1116,7 +1118,9 @@ hipError_t launch_paged_mq(const MqParams& p, int ncb, hipStream_t stream) {
   if (e != hipSuccess) return e;
   if (p.max_parts > 1) {
     if (p.cu_q != nullptr) {
-      hipLaunchKernelGGL(mq_reduce_varlen_kernel, dim3((unsigned)p.num_seqs), dim3(256), 0, stream, p);
+      const int64_t wgs = (int64_t)p.num_seqs * merge_slices(p, 4);
+      if (wgs > 0x7fffffff) return hipErrorInvalidValue;
+      hipLaunchKernelGGL(mq_reduce_varlen_kernel, dim3((unsigned)wgs), dim3(256), 0, stream, p);
     } else {
       const int64_t waves = (int64_t)p.num_seqs * p.Hq;
       hipLaunchKernelGGL(mq_reduce_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream, p);

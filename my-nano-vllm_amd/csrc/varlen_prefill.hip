@@ -119,10 +119,12 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kBufElems];
 
   // Workgroups past the items merge the split-KV partitions of the
-  // short-query sequences (one sequence each), which the launch before this
-  // one computed.
+  // short-query sequences, which the launch before this one computed: one
+  // (row, head) pair per wave.
   if ((int)blockIdx.x >= n_main) {
-    merge_varlen_seq(mq, (int)blockIdx.x - n_main, wave_uniform(threadIdx.x >> 6), kPrefillWaves, threadIdx.x & 63);
+    const int slices = merge_slices(mq, kPrefillWaves);
+    const int m = (int)blockIdx.x - n_main, seq = m / slices;
+    merge_varlen_one(mq, seq, (m - seq * slices) * kPrefillWaves + (int)(threadIdx.x >> 6), threadIdx.x & 63);
     return;
   }
 
@@ -592,7 +594,7 @@ hipError_t launch_varlen_prefill(const PrefillParams& p, const void* schedule, c
   if (p.num_seqs == 0 || p.n_mblocks == 0) return hipSuccess;
   const int64_t n_items_max = (int64_t)p.num_seqs * p.n_mblocks;
   const int64_t n_blocks = n_items_max * p.Hkv * p.n_hgroups;
-  const int64_t n_merge = merge ? mq.num_seqs : 0;
+  const int64_t n_merge = merge ? (int64_t)mq.num_seqs * merge_slices(mq, kPrefillWaves) : 0;
   if (n_blocks + n_merge > 0x7fffffff || schedule == nullptr) return hipErrorInvalidValue;
   const dim3 grid((unsigned)(n_blocks + n_merge)), block(64 * kPrefillWaves);
   const PrefillItem* items = static_cast<const PrefillItem*>(schedule);
