@@ -128,8 +128,10 @@ int64_t nvamd_prefill_workspace_bytes(int64_t num_tokens, int32_t num_seqs, int3
  * max_seqlen_q bounds Lq (host value, as in the reference's grid);
  *   max_seqlen_k is accepted for signature parity and not needed.
  * Short-query sequences (Lq * num_heads/num_kv_heads <= 32, e.g. speculative
- * decode verification) run on the split-KV decode kernel; longer ones on
- * the MFMA prefill kernel.
+ * decode verification) run on a decode kernel: the balanced (stream-K) one
+ * for the paged layout when decode would use it (part_tokens = 0,
+ * num_kv_heads % 4 == 0), else the split-KV one; longer ones on the MFMA
+ * prefill kernel.
  */
 int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, const void* v,
                                     const int32_t* block_tables,

@@ -93,18 +93,25 @@ bool use_stream_k(int32_t batch, int32_t num_kv_heads, int32_t part_tokens) {
   return part_tokens == 0 && num_kv_heads % 4 == 0 && batch <= nvamd::kSkMaxSeqs;
 }
 
+// Query columns per kv head of the short-query rows of a varlen call.
+int short_cols(int G, int32_t max_seqlen_q) { return G * std::min(32 / G, std::max(max_seqlen_q, 1)); }
+
 // kv heads per balanced-decode workgroup: whole 1 KiB cache rows when the
 // kv heads come in 8s (each workgroup then reads whole DRAM pages), else 4.
 int stream_k_heads(int32_t num_kv_heads) { return num_kv_heads % 8 == 0 ? 8 : 4; }
 
-int stream_k_wgs(int ncb, int hg, int G) { return device_cu_count() * nvamd::decode_sk_wgs_per_cu(ncb, hg, G); }
+int stream_k_wgs(int ncb, int hg, int G, bool varlen) {
+  return device_cu_count() * nvamd::decode_sk_wgs_per_cu(ncb, hg, G, varlen);
+}
 
-// Workspace of the balanced decode: the stage prefix, then the partial slots.
+// Workspace of the balanced kernel: the stage prefix, then the partial slots
+// (cols query columns per kv head: G for decode, G * mq_max_q for the
+// short-query rows of a varlen call).
 int64_t stream_k_prefix_bytes(int32_t batch) { return (((int64_t)batch + 1) * 4 + 255) / 256 * 256; }
-int64_t stream_k_bytes(int32_t batch, int32_t num_kv_heads, int32_t G) {
-  const int ncb = (G + 15) / 16, hg = stream_k_heads(num_kv_heads);
+int64_t stream_k_bytes(int32_t batch, int32_t num_kv_heads, int32_t G, int cols, bool varlen) {
+  const int ncb = (cols + 15) / 16, hg = stream_k_heads(num_kv_heads);
   return stream_k_prefix_bytes(batch) +
-         (int64_t)stream_k_wgs(ncb, hg, G) * 2 * hg * G * nvamd::kSkSlotFloats * (int64_t)sizeof(float);
+         (int64_t)stream_k_wgs(ncb, hg, G, varlen) * 2 * hg * cols * nvamd::kSkSlotFloats * (int64_t)sizeof(float);
 }
 
 void set_partials(nvamd::MqParams& p, void* workspace) {
@@ -178,7 +185,7 @@ int64_t nvamd_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t n
     return 0;
   if (num_heads % num_kv_heads != 0) return 0;
   if (use_stream_k(batch, num_kv_heads, part_tokens))
-    return stream_k_bytes(batch, num_kv_heads, num_heads / num_kv_heads);
+    return stream_k_bytes(batch, num_kv_heads, num_heads / num_kv_heads, num_heads / num_kv_heads, false);
   const int64_t kv_cap = (int64_t)max_num_blocks * block_size;
   const int64_t part = choose_part_tokens((int64_t)batch * kv_head_groups(num_kv_heads), kv_cap,
                                           part_tokens, block_size);
@@ -234,17 +241,18 @@ int32_t nvamd_fp8_decode_attention(void* out, const void* q, const void* k_cache
   p.scale_log2 = softmax_scale * 1.4426950408889634f;
   const int ncb = (G + 15) / 16;
   if (use_stream_k(batch, num_kv_heads, part_tokens)) {
-    const int64_t need = stream_k_bytes(batch, num_kv_heads, G);
+    const int64_t need = stream_k_bytes(batch, num_kv_heads, G, G, false);
     if (workspace == nullptr || workspace_bytes < need)
       return fail(NVAMD_ERR_WORKSPACE, "%s: workspace of %lld bytes required (got %lld)", fn,
                   (long long)need, (long long)workspace_bytes);
     p.part_tokens = (int)std::min<int64_t>(kv_cap, 0x7fffffff);
     p.max_parts = 1;
     p.sk_heads = stream_k_heads(num_kv_heads);
-    p.sk_wgs = stream_k_wgs(ncb, p.sk_heads, G);
+    p.sk_wgs = stream_k_wgs(ncb, p.sk_heads, G, false);
+    p.sk_cols = G;
     p.sk_prefix = static_cast<int32_t*>(workspace);
     p.sk_part = reinterpret_cast<float*>(static_cast<char*>(workspace) + stream_k_prefix_bytes(batch));
-    return launch_status(nvamd::launch_decode_sk(p, ncb, (hipStream_t)stream), fn);
+    return launch_status(nvamd::launch_decode_sk(p, ncb, true, (hipStream_t)stream), fn);
   }
   const int64_t part = choose_part_tokens((int64_t)batch * kv_head_groups(num_kv_heads), kv_cap,
                                           part_tokens, block_size);
@@ -266,7 +274,9 @@ int64_t nvamd_prefill_workspace_bytes(int64_t num_tokens, int32_t num_seqs, int3
   if (G <= 0 || G > kMqMaxCols) return 0;
   const int64_t part = choose_part_tokens((int64_t)num_seqs * kv_head_groups(num_kv_heads), kv_cap,
                                           part_tokens, block_size);
-  const int64_t partials = partial_bytes(num_tokens, num_heads, ceil_div(kv_cap, part));
+  int64_t partials = partial_bytes(num_tokens, num_heads, ceil_div(kv_cap, part));
+  if (block_size > 0 && use_stream_k(num_seqs, num_kv_heads, part_tokens))  // paged: the balanced kernel
+    partials = stream_k_bytes(num_seqs, num_kv_heads, G, short_cols(G, max_seqlen_q), true);
   return align_up(partials) + schedule_bytes(num_seqs, G, max_seqlen_q);
 }
 
@@ -306,7 +316,11 @@ int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, con
   const int64_t kv_cap = paged ? (int64_t)max_num_blocks * block_size : std::max<int64_t>(num_kv_rows, 1);
   const int64_t part = choose_part_tokens((int64_t)num_seqs * kv_head_groups(num_kv_heads), kv_cap,
                                           part_tokens, paged ? block_size : 0);
-  const int64_t partials = partial_bytes(num_tokens, num_heads, ceil_div(kv_cap, part));
+  // Short-query rows of a paged call take the balanced (stream-K) kernel
+  // when decode would; otherwise the split-KV kernel.
+  const bool sk = paged && use_stream_k(num_seqs, num_kv_heads, part_tokens);
+  const int64_t partials = sk ? stream_k_bytes(num_seqs, num_kv_heads, G, short_cols(G, max_seqlen_q), true)
+                              : partial_bytes(num_tokens, num_heads, ceil_div(kv_cap, part));
   const int64_t sched = schedule_bytes(num_seqs, G, max_seqlen_q);
   const int64_t need = align_up(partials) + sched;
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
@@ -335,10 +349,27 @@ int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, con
   mp.max_parts = (int)ceil_div(kv_cap, part);
   mp.mq_max_q = std::min(mq_max_q, max_seqlen_q);
   mp.scale_log2 = softmax_scale * 1.4426950408889634f;
-  set_partials(mp, partials > 0 ? workspace : nullptr);
   const int ncb = (G * mp.mq_max_q + 15) / 16;
-  if (max_seqlen_q <= mq_max_q)  // short sequences only: the split-KV kernel and its merge
-    return launch_status(nvamd::launch_paged_mq(mp, ncb, (hipStream_t)stream), fn);
+  if (sk) {
+    mp.part_tokens = (int)std::min<int64_t>(kv_cap, 0x7fffffff);
+    mp.max_parts = 1;
+    mp.sk_heads = stream_k_heads(num_kv_heads);
+    mp.sk_wgs = stream_k_wgs(ncb, mp.sk_heads, G, true);
+    mp.sk_cols = short_cols(G, max_seqlen_q);
+    mp.sk_prefix = static_cast<int32_t*>(workspace);
+    mp.sk_part = reinterpret_cast<float*>(static_cast<char*>(workspace) + stream_k_prefix_bytes(num_seqs));
+    // balanced pass over the short-query rows (sequences with longer query
+    // runs take no stages and are left alone); its merge is a launch of its
+    // own when every sequence is short, else extra workgroups of the
+    // prefill kernel
+    const bool all_short = max_seqlen_q <= mq_max_q;
+    const hipError_t e = nvamd::launch_decode_sk(mp, ncb, all_short, (hipStream_t)stream);
+    if (e != hipSuccess || all_short) return launch_status(e, fn);
+  } else {
+    set_partials(mp, partials > 0 ? workspace : nullptr);
+    if (max_seqlen_q <= mq_max_q)  // short sequences only: the split-KV kernel and its merge
+      return launch_status(nvamd::launch_paged_mq(mp, ncb, (hipStream_t)stream), fn);
+  }
 
   // Longer sequences: MFMA prefill kernel.  Two launches: the short-query
   // pass (which also writes the prefill work list), then the prefill kernel
@@ -368,9 +399,14 @@ int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, con
   pp.mq_max_q = mq_max_q;
   pp.scale_log2 = softmax_scale * 1.4426950408889634f;
   void* schedule = static_cast<char*>(workspace) + align_up(partials);
-  hipError_t e = nvamd::launch_prefill_short(mp, ncb, pp, schedule, (hipStream_t)stream);
+  // After the balanced pass the short-query launch only writes the work
+  // list (no sequence is short to it); the prefill kernel merges either
+  // pass's partials.
+  nvamd::MqParams mq_short = mp;
+  if (sk) mq_short.mq_max_q = 0;
+  hipError_t e = nvamd::launch_prefill_short(mq_short, ncb, pp, schedule, (hipStream_t)stream);
   if (e != hipSuccess) return launch_status(e, fn);
-  e = nvamd::launch_varlen_prefill(pp, schedule, mp, mp.max_parts > 1, (hipStream_t)stream);
+  e = nvamd::launch_varlen_prefill(pp, schedule, mp, sk || mp.max_parts > 1, (hipStream_t)stream);
   if (e != hipSuccess) return launch_status(e, fn);
   return ok();
 }

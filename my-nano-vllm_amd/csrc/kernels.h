@@ -28,10 +28,11 @@ struct MqParams {
   int mq_max_q;                 // varlen mode: only sequences with 1 <= Lq <= mq_max_q
   float scale_log2;
   // Balanced decode (stream-K over KV stages), see decode_sk_kernel.
-  float* sk_part;               // [sk_wgs, 2, sk_heads, G, kSkSlotFloats] partial (acc, m, l)
+  float* sk_part;               // [sk_wgs, 2, sk_heads, sk_cols, kSkSlotFloats] partial (acc, m, l)
   int32_t* sk_prefix;           // [num_seqs + 1] stages per kv-head group before each sequence
   int sk_wgs;                   // persistent workgroups
   int sk_heads;                 // kv heads per workgroup (4 or 8; one wave each)
+  int sk_cols;                  // query columns per kv head: G (decode) or G * mq_max_q (varlen)
 };
 
 // Balanced decode: 16-token stages.
@@ -74,8 +75,8 @@ hipError_t launch_kv_store(const void* key, int64_t key_stride, const void* valu
 
 hipError_t launch_paged_mq(const MqParams& p, int ncb, hipStream_t stream);
 // Persistent workgroups the balanced decode kernel keeps resident per CU.
-int decode_sk_wgs_per_cu(int ncb, int hg, int G);
-hipError_t launch_decode_sk(const MqParams& p, int ncb, hipStream_t stream);
+int decode_sk_wgs_per_cu(int ncb, int hg, int G, bool varlen);
+hipError_t launch_decode_sk(const MqParams& p, int ncb, bool merge, hipStream_t stream);
 
 // Device bytes of the prefill work list (sorted items).
 int64_t prefill_schedule_bytes(const PrefillParams& p);

@@ -1,6 +1,7 @@
-// Log-sum-exp merge of split-KV partitions (shared by the short-query /
-// decode passes and the prefill kernel, which merges the short-query rows of
-// a prefill call in extra workgroups instead of a launch of its own).
+// Log-sum-exp merges of split-KV partitions and of the balanced kernel's cut
+// pairs (shared by the merge launches and the prefill kernel, which merges
+// the short-query rows of a prefill call in extra workgroups instead of a
+// launch of its own).
 #pragma once
 
 #include "fp8_common.h"
@@ -87,6 +88,105 @@ __device__ __forceinline__ void merge_varlen_one(const MqParams& p, int seq, int
 // merge launch needs per sequence.
 __host__ __device__ __forceinline__ int merge_slices(const MqParams& p, int n_waves) {
   return (p.mq_max_q * p.Hq + n_waves - 1) / n_waves;
+}
+
+// ---- balanced (stream-K) kernel: merge of a pair cut across workgroups ----
+
+// Workgroup holding stage x of T split over W workgroups.
+__device__ __forceinline__ int sk_owner(int64_t x, int64_t T, int W) {
+  return (int)(((x + 1) * W + T - 1) / T) - 1;
+}
+
+// Merges the partials of one (query row, head) whose pair was cut across
+// workgroups, or zero-fills it when its context is empty; one wave: row
+// idx / Hq of sequence b (the only row in decode), head idx % Hq.  Lane i
+// reads (m, l) of the i-th contributing workgroup, the wave reduces them,
+// then every lane accumulates 2 dims over the contributions.
+__device__ __forceinline__ void sk_merge_one(const MqParams& p, int b, int idx, int lane) {
+  if (b >= p.num_seqs || idx >= p.mq_max_q * p.Hq) return;
+  const int qr = idx / p.Hq, hq = idx - qr * p.Hq;
+  int64_t q0 = b;
+  if (p.cu_q != nullptr) {  // varlen: short-query sequences only
+    q0 = p.cu_q[b];
+    const int lq = p.cu_q[b + 1] - (int)q0;
+    if (lq <= 0 || lq > p.mq_max_q || qr >= lq || q0 + qr >= p.q_rows) return;
+  }
+  const int G = p.G, HG = p.sk_heads, NHG = p.Hkv / HG;
+  const int kvh = hq / G, col = qr * G + (hq - kvh * G);
+  const int hg = kvh / HG, hh = kvh - hg * HG;
+  // the pair's stage count and position come from the prefix the main pass
+  // wrote (loads independent of each other and of cu_q: one round trip)
+  const int pre_b = p.sk_prefix[b];
+  const int n = p.sk_prefix[b + 1] - pre_b;
+  uint32_t* out = reinterpret_cast<uint32_t*>(p.out + ((q0 + qr) * p.Hq + hq) * kHeadDim);
+  if (n == 0) {
+    // Empty context (graph padding rows): the reference yields NaN here; write 0.
+    out[lane] = 0u;
+    return;
+  }
+  const int W = p.sk_wgs;
+  const int64_t T = (int64_t)NHG * p.sk_prefix[p.num_seqs];
+  const int64_t P = (int64_t)NHG * pre_b + (int64_t)hg * n;
+  const int wf = sk_owner(P, T, W), wl = sk_owner(P + n - 1, T, W);
+  if (wf == wl) return;  // finished by its workgroup
+  // Workgroups in (wf, wl] start inside the pair, so it is their first pair
+  // (slot 0); wf holds it in slot 0 if its range starts at P, else in slot 1
+  // (its last pair).  With T >= W no range is empty; otherwise workgroups
+  // with empty ranges wrote nothing and are skipped.  (64-bit divisions are
+  // long instruction sequences: one per contributor made this pass
+  // instruction-bound when pairs are cut many times.)
+  const int slot_f = ((int64_t)wf * T / W < P) ? 1 : 0;
+  const bool may_be_empty = T < W;
+  auto slot_ptr = [&](int w) -> const float* {
+    if (may_be_empty && (int64_t)w * T / W == (int64_t)(w + 1) * T / W) return nullptr;
+    const int slot = (w == wf) ? slot_f : 0;
+    return p.sk_part + ((((int64_t)w * 2 + slot) * HG + hh) * p.sk_cols + col) * kSkSlotFloats;
+  };
+  // Contributors in chunks of 8: all of a chunk's loads (lane j < 8 reads
+  // (m, l) of contributor j, every lane its 2 dims of each) are issued
+  // before any is used, so a chunk costs one memory round trip.
+  float M = -INFINITY, Lsum = 0.f, o0 = 0.f, o1 = 0.f;
+  for (int w0 = wf; w0 <= wl; w0 += 8) {
+    const int cnt = min(8, wl - w0 + 1);
+    float mi = -INFINITY, li = 0.f;
+    f32x2 a[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      a[j] = f32x2{0.f, 0.f};
+      const float* ps = (j < cnt) ? slot_ptr(w0 + j) : nullptr;
+      if (ps != nullptr) {
+        a[j] = *reinterpret_cast<const f32x2*>(ps + 2 * lane);
+        if (lane == j) {
+          mi = ps[kHeadDim];
+          li = ps[kHeadDim + 1];
+        }
+      }
+    }
+    float Mp = mi;
+#pragma unroll
+    for (int off = 4; off > 0; off >>= 1) Mp = fmaxf(Mp, shfl_xor_f32(Mp, off));
+    Mp = __shfl(Mp, 0, 64);  // lanes 0..7 hold the chunk's values
+    const float Mn = fmaxf(M, Mp);
+    const float Ms = (Mn == -INFINITY) ? 0.f : Mn;
+    const float sc = (M == -INFINITY) ? 0.f : fast_exp2(M - Ms);
+    Lsum *= sc;
+    o0 *= sc;
+    o1 *= sc;
+    M = Mn;
+    const float wi = (mi == -INFINITY) ? 0.f : fast_exp2(mi - Ms);
+    float lw = li * wi;
+#pragma unroll
+    for (int off = 4; off > 0; off >>= 1) lw += shfl_xor_f32(lw, off);
+    Lsum += __shfl(lw, 0, 64);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float wk = __shfl(wi, j, 64);
+      o0 += wk * a[j].x;
+      o1 += wk * a[j].y;
+    }
+  }
+  const float inv = (Lsum > 0.f) ? 1.0f / Lsum : 0.f;
+  out[lane] = out_round_bf16_bits(o0 * inv) | (out_round_bf16_bits(o1 * inv) << 16);
 }
 
 }  // namespace nvamd

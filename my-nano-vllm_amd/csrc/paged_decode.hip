@@ -596,7 +596,10 @@ __global__ __launch_bounds__(256) void mq_reduce_varlen_kernel(MqParams p) {
 // ---------------------------------------------------------------------------
 // Balanced decode: stream-K over KV stages
 // ---------------------------------------------------------------------------
-// Pure decode (one query row per sequence) with Hkv % 4 == 0.  A pair =
+// Pure decode (one query row per sequence) with Hkv % 4 == 0, and the
+// short-query sequences of a paged varlen call (speculative-decode rows:
+// the Lq * G <= 32 query rows of a kv head are its MFMA columns, each with
+// its causal key limit; other sequences take no stages).  A pair =
 // (sequence b, group hg of HG kv heads, HG = 8 when Hkv % 8 == 0, else 4);
 // its n_b = ceil(L_b / 16) stages of 16 tokens are laid end to end in
 // (b, hg) order, T stages in all.  Workgroup w of a persistent grid of W
@@ -619,16 +622,25 @@ __device__ __forceinline__ int sload_i32(const int32_t* base, int64_t i) {
   return ((const __attribute__((address_space(4))) int32_t*)base)[i];
 }
 
-// Workgroup holding stage x of T split over W workgroups.
-__device__ __forceinline__ int sk_owner(int64_t x, int64_t T, int W) {
-  return (int)(((x + 1) * W + T - 1) / T) - 1;
-}
 
 __device__ __forceinline__ int sk_capacity(const MqParams& p) {
   return (int)min(p.bt_stride * (int64_t)p.block_size, (int64_t)0x7fffffff);
 }
 
 __device__ __forceinline__ int sk_stages(int L) { return L > 0 ? (L + kSkStageTokens - 1) / kSkStageTokens : 0; }
+
+// Keys of sequence b in the stage space: its context (decode) or, in varlen
+// mode, its key count when it is a short-query sequence (1 <= Lq <=
+// mq_max_q); the other sequences take no stages.  SCALAR reads the tables
+// through the scalar data cache (b wave-uniform).
+template <bool SCALAR>
+__device__ __forceinline__ int sk_seq_len(const MqParams& p, int b, int cap) {
+  auto rd = [&](const int32_t* t, int i) { return SCALAR ? sload_i32(t, i) : t[i]; };
+  if (p.cu_q == nullptr) return min(rd(p.context_lens, b), cap);
+  const int lq = rd(p.cu_q, b + 1) - rd(p.cu_q, b);
+  if (lq <= 0 || lq > p.mq_max_q) return 0;
+  return max(0, min(rd(p.cu_k, b + 1) - rd(p.cu_k, b), cap));
+}
 
 // Stage of the balanced kernel: 16 token rows of HG*128 bytes (K, then V),
 // fetched by 64*HG lanes as 2*HG 1 KiB direct-to-LDS loads per half.  With
@@ -680,7 +692,7 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p) {
   int carry = 0;
   for (int base = 0; base < B; base += kThreads) {
     const int b = base + tid;
-    const int L = (b < B) ? min(p.context_lens[b], cap) : 0;
+    const int L = (b < B) ? sk_seq_len<false>(p, b, cap) : 0;
     if (b < B) lens[b] = L;
     const int n = sk_stages(L);
     int incl = n;
@@ -716,6 +728,13 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p) {
   const int hg0 = (int)(rem / n0), o0 = (int)(rem - (int64_t)hg0 * n0);
   const int n_w = (int)(end - start);
   const int L0 = lens[b0];
+  // varlen: the first pair's query rows, read here so that the read overlaps
+  // the block-table reads of the first stage
+  int q0_first = b0, lq_first = 1;
+  if (p.cu_q != nullptr) {
+    q0_first = sload_i32(p.cu_q, b0);
+    lq_first = sload_i32(p.cu_q, b0 + 1) - q0_first;
+  }
   __syncthreads();  // the prefix is read; the ring is about to be filled
 
   const int64_t rs = (int64_t)p.Hkv * kHeadDim;  // bytes between token rows
@@ -751,7 +770,7 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p) {
       hg = 0;
       do {
         ++b;
-        L = (b < B) ? min(sload_i32(p.context_lens, b), cap) : 0;
+        L = (b < B) ? sk_seq_len<true>(p, b, cap) : 0;
         n = sk_stages(L);
       } while (n == 0 && b < B - 1);
     }
@@ -826,25 +845,44 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p) {
   int seg_o0 = o0;
   bf16x8 qop[NCB][4];
   int col_limit[NCB];
+  int64_t col_row[NCB];  // output / query element offset of the lane's column, -1 if unused
+  int mask_from = 0;     // first key position that some column of the pair cannot see
   float m[NCB], lsum[NCB];
   f32x4 acc[NCB][8];
   // New pair: reset the softmax state; the queries are read here from
   // global memory (!QL: the wait drains the stages in flight) or, with QL,
   // from the query area of the pair's first stage once it has landed.
+  // Column c of kv head kvh is query row c / G (of the sequence's Lq rows;
+  // Lq = 1 in decode) of head kvh * G + c % G, and sees the keys before
+  // L - Lq + 1 + c / G (causal within the new rows).
   bool q_from_lds = false;
   auto begin_pair = [&]() {
     const int kvh = chg * HG + wave;
+    int64_t q0 = cb_s;
+    int lq = 1;
+    if (p.cu_q != nullptr) {
+      if (cb_s == b0) {  // read in the prologue
+        q0 = q0_first;
+        lq = lq_first;
+      } else {
+        q0 = sload_i32(p.cu_q, cb_s);
+        lq = sload_i32(p.cu_q, cb_s + 1) - (int)q0;
+      }
+    }
+    mask_from = cL - lq + 1;
 #pragma unroll
     for (int cb = 0; cb < NCB; ++cb) {
       const int col = 16 * cb + r;
-      const bool valid = col < G;
-      col_limit[cb] = valid ? cL : 0;
+      const int qr = col / G, j = col - qr * G;
+      const bool valid = qr < lq && q0 + qr < p.q_rows;
+      col_limit[cb] = valid ? cL - lq + 1 + qr : 0;
+      col_row[cb] = valid ? ((q0 + qr) * p.Hq + kvh * G + j) * kHeadDim : -1;
       if (!QL) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           u32x4 a = {0u, 0u, 0u, 0u}, b = {0u, 0u, 0u, 0u};
           if (valid) {
-            const uint16_t* qp = p.q + ((int64_t)cb_s * p.Hq + kvh * G + col) * kHeadDim + 16 * gam + 64 * h;
+            const uint16_t* qp = p.q + col_row[cb] + 16 * gam + 64 * h;
             a = *reinterpret_cast<const u32x4*>(qp);
             b = *reinterpret_cast<const u32x4*>(qp + 8);
           }
@@ -881,16 +919,15 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p) {
   };
   // Writes the output of a pair finished here, or the partial of a cut pair.
   auto end_segment = [&](bool full) {
-    const int kvh = chg * HG + wave;
 #pragma unroll
     for (int cb = 0; cb < NCB; ++cb) {
       lsum[cb] += shfl_xor_f32(lsum[cb], 16);
       lsum[cb] += shfl_xor_f32(lsum[cb], 32);
       const int col = 16 * cb + r;
-      if (col >= G) continue;
+      if (col_row[cb] < 0) continue;
       if (full) {
         const float inv = (lsum[cb] > 0.f) ? 1.0f / lsum[cb] : 0.f;
-        uint16_t* op = p.out + ((int64_t)cb_s * p.Hq + kvh * G + col) * kHeadDim + 32 * gam;
+        uint16_t* op = p.out + col_row[cb] + 32 * gam;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           float o[8];
@@ -900,7 +937,7 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p) {
         }
       } else {
         const int slot = first_seg ? 0 : 1;
-        float* ps = p.sk_part + ((((int64_t)w * 2 + slot) * HG + wave) * G + col) * kSkSlotFloats;
+        float* ps = p.sk_part + ((((int64_t)w * 2 + slot) * HG + wave) * p.sk_cols + col) * kSkSlotFloats;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           *reinterpret_cast<f32x4*>(ps + 32 * gam + 8 * k) =
@@ -918,9 +955,9 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p) {
 
   constexpr int D = S::kDepth;
   seek_block();
-  begin_pair();
 #pragma unroll
   for (int i = 0; i < D - 1; ++i) issue_stage(i);
+  begin_pair();  // after the first stages are issued: a global query load overlaps them
   for (int s = 0; s < n_w; ++s) {
     wait_vmcnt<4 * (D - 2)>();  // this wave's loads of stage s have landed (the 4 of each later stage may not)
     lds_barrier();              // ... and every wave's; slot (s-1)%D is no longer being read
@@ -936,7 +973,7 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) cr.v[e] = lds_read8(sl + v_rd[e]);
     const int tok0 = co * kSkStageTokens;
-    attend_chunk<NCB>(cr, qop, col_limit, tok0, tok0 + kSkStageTokens > cL, p.scale_log2, gam, m, lsum, acc);
+    attend_chunk<NCB>(cr, qop, col_limit, tok0, tok0 + kSkStageTokens > mask_from, p.scale_log2, gam, m, lsum, acc);
     if (++co == cn || s == n_w - 1) {
       end_segment(seg_o0 == 0 && co == cn);
       if (s < n_w - 1) {
@@ -951,84 +988,15 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p) {
   wait_vmcnt<0>();  // nothing may land in LDS after the workgroup exits
 }
 
-// Merges the partials of one pair cut across workgroups (or zero-fills a
-// row with an empty context).  One wave per (sequence, query head): lane i
-// reads (m, l) of the i-th contributing workgroup, the wave reduces them,
-// then every lane accumulates 2 dims over the contributions.
+// One wave per (sequence, query row, head): wave -> (sequence b, index of
+// its mq_max_q * Hq (row, head) pairs); decode has one row per sequence
+// (mq_max_q = 1).
 __global__ __launch_bounds__(256) void decode_sk_merge_kernel(MqParams p) {
-  const int lane = threadIdx.x & 63;
   const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (gw >= (int64_t)p.num_seqs * p.Hq) return;
-  const int b = (int)(gw / p.Hq), hq = (int)(gw - (int64_t)b * p.Hq);
-  const int G = p.G, HG = p.sk_heads, NHG = p.Hkv / HG;
-  const int kvh = hq / G, col = hq - kvh * G;
-  const int hg = kvh / HG, hh = kvh - hg * HG;
-  const int L = min(p.context_lens[b], sk_capacity(p));
-  const int n = sk_stages(L);
-  uint32_t* out = reinterpret_cast<uint32_t*>(p.out + gw * kHeadDim);
-  if (n == 0) {
-    // Empty context (graph padding rows): the reference yields NaN here; write 0.
-    out[lane] = 0u;
-    return;
-  }
-  const int W = p.sk_wgs;
-  const int64_t T = (int64_t)NHG * p.sk_prefix[p.num_seqs];
-  const int64_t P = (int64_t)NHG * p.sk_prefix[b] + (int64_t)hg * n;
-  const int wf = sk_owner(P, T, W), wl = sk_owner(P + n - 1, T, W);
-  if (wf == wl) return;  // finished by its workgroup
-  // Workgroups in (wf, wl] start inside the pair; those with empty ranges
-  // (more workgroups than stages) wrote nothing and are skipped.
-  auto slot_ptr = [&](int w) -> const float* {
-    const int64_t s0 = (int64_t)w * T / W;
-    if (s0 == (int64_t)(w + 1) * T / W) return nullptr;
-    const int slot = (s0 < P) ? 1 : 0;
-    return p.sk_part + ((((int64_t)w * 2 + slot) * HG + hh) * G + col) * kSkSlotFloats;
-  };
-  // Contributors in chunks of 8: all of a chunk's loads (lane j < 8 reads
-  // (m, l) of contributor j, every lane its 2 dims of each) are issued
-  // before any is used, so a chunk costs one memory round trip.
-  float M = -INFINITY, Lsum = 0.f, o0 = 0.f, o1 = 0.f;
-  for (int w0 = wf; w0 <= wl; w0 += 8) {
-    const int cnt = min(8, wl - w0 + 1);
-    float mi = -INFINITY, li = 0.f;
-    f32x2 a[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      a[j] = f32x2{0.f, 0.f};
-      const float* ps = (j < cnt) ? slot_ptr(w0 + j) : nullptr;
-      if (ps != nullptr) {
-        a[j] = *reinterpret_cast<const f32x2*>(ps + 2 * lane);
-        if (lane == j) {
-          mi = ps[kHeadDim];
-          li = ps[kHeadDim + 1];
-        }
-      }
-    }
-    float Mp = mi;
-#pragma unroll
-    for (int off = 4; off > 0; off >>= 1) Mp = fmaxf(Mp, shfl_xor_f32(Mp, off));
-    Mp = __shfl(Mp, 0, 64);  // lanes 0..7 hold the chunk's values
-    const float Mn = fmaxf(M, Mp);
-    const float Ms = (Mn == -INFINITY) ? 0.f : Mn;
-    const float sc = (M == -INFINITY) ? 0.f : fast_exp2(M - Ms);
-    Lsum *= sc;
-    o0 *= sc;
-    o1 *= sc;
-    M = Mn;
-    const float wi = (mi == -INFINITY) ? 0.f : fast_exp2(mi - Ms);
-    float lw = li * wi;
-#pragma unroll
-    for (int off = 4; off > 0; off >>= 1) lw += shfl_xor_f32(lw, off);
-    Lsum += __shfl(lw, 0, 64);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float wk = __shfl(wi, j, 64);
-      o0 += wk * a[j].x;
-      o1 += wk * a[j].y;
-    }
-  }
-  const float inv = (Lsum > 0.f) ? 1.0f / Lsum : 0.f;
-  out[lane] = out_round_bf16_bits(o0 * inv) | (out_round_bf16_bits(o1 * inv) << 16);
+  const int per_seq = p.mq_max_q * p.Hq;
+  if (gw >= (int64_t)p.num_seqs * per_seq) return;
+  const int b = (int)(gw / per_seq);
+  sk_merge_one(p, b, (int)(gw - (int64_t)b * per_seq), threadIdx.x & 63);
 }
 
 namespace {
@@ -1045,15 +1013,16 @@ int sk_occupancy() {
 }
 
 // Instantiation: 0 = <1,4,-> 1 = <2,4,-> 2 = <1,8,QL> 3 = <1,8,-> 4 = <2,8,->
-int sk_variant(int ncb, int hg, int G) {
+// (queries through LDS only for decode: one query row per sequence)
+int sk_variant(int ncb, int hg, int G, bool varlen) {
   if (hg == 4) return ncb == 1 ? 0 : 1;
   if (ncb == 2) return 4;
-  return G <= kSkQMaxG ? 2 : 3;
+  return (G <= kSkQMaxG && !varlen) ? 2 : 3;
 }
 }  // namespace
 
-int decode_sk_wgs_per_cu(int ncb, int hg, int G) {
-  switch (sk_variant(ncb, hg, G)) {
+int decode_sk_wgs_per_cu(int ncb, int hg, int G, bool varlen) {
+  switch (sk_variant(ncb, hg, G, varlen)) {
     case 0: return sk_occupancy<1, 4, false>();
     case 1: return sk_occupancy<2, 4, false>();
     case 2: return sk_occupancy<1, 8, true>();
@@ -1062,14 +1031,18 @@ int decode_sk_wgs_per_cu(int ncb, int hg, int G) {
   }
 }
 
-hipError_t launch_decode_sk(const MqParams& p, int ncb, hipStream_t stream) {
+hipError_t launch_decode_sk(const MqParams& p, int ncb, bool merge, hipStream_t stream) {
   if (p.num_seqs == 0) return hipSuccess;
   const int hg = p.sk_heads;
-  if ((hg != 4 && hg != 8) || p.Hkv % hg != 0 || p.num_seqs > kSkMaxSeqs || p.sk_wgs <= 0 || p.cu_q != nullptr ||
-      (ncb != 1 && ncb != 2))
+  const bool varlen = p.cu_q != nullptr;
+  if ((hg != 4 && hg != 8) || p.Hkv % hg != 0 || p.num_seqs > kSkMaxSeqs || p.sk_wgs <= 0 ||
+      (ncb != 1 && ncb != 2) || p.mq_max_q < 1 || p.G * p.mq_max_q > 16 * ncb || p.sk_cols < p.G * p.mq_max_q ||
+      (varlen && p.cu_k == nullptr) || (!varlen && (p.mq_max_q != 1 || p.context_lens == nullptr)))
     return hipErrorInvalidValue;
+  const int64_t merge_wgs = ((int64_t)p.num_seqs * p.mq_max_q * p.Hq + 3) / 4;  // one wave per (row, head)
+  if (merge_wgs > 0x7fffffff) return hipErrorInvalidValue;
   const dim3 grid((unsigned)p.sk_wgs), block((unsigned)(64 * hg));
-  switch (sk_variant(ncb, hg, p.G)) {
+  switch (sk_variant(ncb, hg, p.G, varlen)) {
     case 0: hipLaunchKernelGGL((decode_sk_kernel<1, 4, false>), grid, block, 0, stream, p); break;
     case 1: hipLaunchKernelGGL((decode_sk_kernel<2, 4, false>), grid, block, 0, stream, p); break;
     case 2: hipLaunchKernelGGL((decode_sk_kernel<1, 8, true>), grid, block, 0, stream, p); break;
@@ -1078,8 +1051,8 @@ hipError_t launch_decode_sk(const MqParams& p, int ncb, hipStream_t stream) {
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int64_t waves = (int64_t)p.num_seqs * p.Hq;
-  hipLaunchKernelGGL(decode_sk_merge_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream, p);
+  if (!merge) return hipSuccess;  // the caller's next launch merges
+  hipLaunchKernelGGL(decode_sk_merge_kernel, dim3((unsigned)merge_wgs), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 

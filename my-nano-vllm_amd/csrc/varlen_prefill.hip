@@ -124,7 +124,9 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
   if ((int)blockIdx.x >= n_main) {
     const int slices = merge_slices(mq, kPrefillWaves);
     const int m = (int)blockIdx.x - n_main, seq = m / slices;
-    merge_varlen_one(mq, seq, (m - seq * slices) * kPrefillWaves + (int)(threadIdx.x >> 6), threadIdx.x & 63);
+    const int idx = (m - seq * slices) * kPrefillWaves + (int)(threadIdx.x >> 6);
+    if (mq.sk_part != nullptr) sk_merge_one(mq, seq, idx, threadIdx.x & 63);  // balanced-kernel partials
+    else merge_varlen_one(mq, seq, idx, threadIdx.x & 63);                    // split-KV partitions
     return;
   }
 

@@ -52,7 +52,7 @@ def test_prefill_mixed_spec_and_chunks():
     _check(wl)
 
 
-@pytest.mark.parametrize("hq,hkv", [(32, 8), (16, 8), (64, 8), (8, 8), (24, 8)])
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (16, 8), (64, 8), (8, 8), (24, 8), (12, 4), (16, 2)])
 def test_prefill_ragged(hq, hkv):
     rng = np.random.default_rng(hq + 7 * hkv)
     lqs = [1, 2, 3, 5, 8, 9, 17, 31, 32, 33, 64, 100, 129, 300]
@@ -84,10 +84,9 @@ def test_prefill_contiguous_equals_paged():
 
 
 def test_prefill_lq1_equals_decode():
-    """Lq = 1 prefill rows (short-query split-KV kernel) against decode (the
-    balanced stream-K kernel at this shape).  Both round P to bf16 against
-    their own running maxima, so they differ by up to a few 1e-3 where the
-    softmax is peaked; each stays within the tolerance of the oracle."""
+    """Lq = 1 prefill rows against decode: at this shape (Hkv % 4 == 0, paged)
+    both run the balanced stream-K kernel over the same stages, so they agree
+    to the last bit; each stays within the tolerance of the oracle."""
     announce("prefill: Lq=1 rows equal decode")
     wl = W.qwen3_0p6b_decode(B=24)
     cpu_c, gpu_c = build_pair(wl)
@@ -99,7 +98,7 @@ def test_prefill_lq1_equals_decode():
                                torch.from_numpy(wl.context_lens()), SCALE)
     assert_close(dec, want, "decode")
     assert_close(pre, want, "Lq=1 prefill")
-    assert_close(pre, dec, "Lq=1 prefill vs decode")
+    assert torch.equal(pre, dec), "Lq=1 prefill vs decode"
 
 
 @pytest.mark.parametrize("bs", [64, 192, 512])
