@@ -252,7 +252,7 @@ int32_t nvamd_fp8_decode_attention(void* out, const void* q, const void* k_cache
     p.sk_cols = G;
     p.sk_prefix = static_cast<int32_t*>(workspace);
     p.sk_part = reinterpret_cast<float*>(static_cast<char*>(workspace) + stream_k_prefix_bytes(batch));
-    return launch_status(nvamd::launch_decode_sk(p, ncb, true, (hipStream_t)stream), fn);
+    return launch_status(nvamd::launch_decode_sk(p, ncb, true, nullptr, nullptr, (hipStream_t)stream), fn);
   }
   const int64_t part = choose_part_tokens((int64_t)batch * kv_head_groups(num_kv_heads), kv_cap,
                                           part_tokens, block_size);
@@ -350,6 +350,7 @@ int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, con
   mp.mq_max_q = std::min(mq_max_q, max_seqlen_q);
   mp.scale_log2 = softmax_scale * 1.4426950408889634f;
   const int ncb = (G * mp.mq_max_q + 15) / 16;
+  const bool all_short = max_seqlen_q <= mq_max_q;
   if (sk) {
     mp.part_tokens = (int)std::min<int64_t>(kv_cap, 0x7fffffff);
     mp.max_parts = 1;
@@ -360,11 +361,9 @@ int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, con
     mp.sk_part = reinterpret_cast<float*>(static_cast<char*>(workspace) + stream_k_prefix_bytes(num_seqs));
     // balanced pass over the short-query rows (sequences with longer query
     // runs take no stages and are left alone); its merge is a launch of its
-    // own when every sequence is short, else extra workgroups of the
-    // prefill kernel
-    const bool all_short = max_seqlen_q <= mq_max_q;
-    const hipError_t e = nvamd::launch_decode_sk(mp, ncb, all_short, (hipStream_t)stream);
-    if (e != hipSuccess || all_short) return launch_status(e, fn);
+    // own when every sequence is short
+    if (all_short)
+      return launch_status(nvamd::launch_decode_sk(mp, ncb, true, nullptr, nullptr, (hipStream_t)stream), fn);
   } else {
     set_partials(mp, partials > 0 ? workspace : nullptr);
     if (max_seqlen_q <= mq_max_q)  // short sequences only: the split-KV kernel and its merge
@@ -399,12 +398,17 @@ int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, con
   pp.mq_max_q = mq_max_q;
   pp.scale_log2 = softmax_scale * 1.4426950408889634f;
   void* schedule = static_cast<char*>(workspace) + align_up(partials);
-  // After the balanced pass the short-query launch only writes the work
-  // list (no sequence is short to it); the prefill kernel merges either
-  // pass's partials.
-  nvamd::MqParams mq_short = mp;
-  if (sk) mq_short.mq_max_q = 0;
-  hipError_t e = nvamd::launch_prefill_short(mq_short, ncb, pp, schedule, (hipStream_t)stream);
+  // The first launch is the short-query pass with one more workgroup that
+  // writes the work list: the balanced kernel (one stream-K workgroup fewer,
+  // so that the work-list workgroup is resident beside the others) or the
+  // split-KV kernel.  The prefill kernel then merges either pass's partials.
+  hipError_t e;
+  if (sk) {
+    mp.sk_wgs = std::max(mp.sk_wgs - 1, 1);
+    e = nvamd::launch_decode_sk(mp, ncb, false, &pp, schedule, (hipStream_t)stream);
+  } else {
+    e = nvamd::launch_prefill_short(mp, ncb, pp, schedule, (hipStream_t)stream);
+  }
   if (e != hipSuccess) return launch_status(e, fn);
   e = nvamd::launch_varlen_prefill(pp, schedule, mp, sk || mp.max_parts > 1, (hipStream_t)stream);
   if (e != hipSuccess) return launch_status(e, fn);

@@ -76,7 +76,9 @@ hipError_t launch_kv_store(const void* key, int64_t key_stride, const void* valu
 hipError_t launch_paged_mq(const MqParams& p, int ncb, hipStream_t stream);
 // Persistent workgroups the balanced decode kernel keeps resident per CU.
 int decode_sk_wgs_per_cu(int ncb, int hg, int G, bool varlen);
-hipError_t launch_decode_sk(const MqParams& p, int ncb, bool merge, hipStream_t stream);
+// pp/items: a prefill call's work list, written by one more workgroup (nullptr: none)
+hipError_t launch_decode_sk(const MqParams& p, int ncb, bool merge, const PrefillParams* pp, void* items,
+                            hipStream_t stream);
 
 // Device bytes of the prefill work list (sorted items).
 int64_t prefill_schedule_bytes(const PrefillParams& p);

@@ -665,8 +665,16 @@ struct SkStage {
   static constexpr int kRing = kDepth * kSlot;
 };
 
+// A prefill call with long sequences launches one workgroup more (index
+// sk_wgs, resident beside the sk_wgs stream-K workgroups) that writes the
+// prefill kernel's work list (items != nullptr).
 template <int NCB, int HG, bool QL>
-__global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p) {
+__global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p, PrefillParams pp, PrefillItem* items,
+                                                            int n_items_max) {
+  if (items != nullptr && (int)blockIdx.x == p.sk_wgs) {
+    prefill_schedule(pp, items, n_items_max);
+    return;
+  }
   using S = SkStage<HG, QL>;
   static_assert(HG == 4 || HG == 8, "4 or 8 kv heads per workgroup");
   static_assert(!QL || NCB == 1, "queries through LDS for G <= 8 only");
@@ -1031,7 +1039,8 @@ int decode_sk_wgs_per_cu(int ncb, int hg, int G, bool varlen) {
   }
 }
 
-hipError_t launch_decode_sk(const MqParams& p, int ncb, bool merge, hipStream_t stream) {
+hipError_t launch_decode_sk(const MqParams& p, int ncb, bool merge, const PrefillParams* pp, void* items,
+                            hipStream_t stream) {
   if (p.num_seqs == 0) return hipSuccess;
   const int hg = p.sk_heads;
   const bool varlen = p.cu_q != nullptr;
@@ -1041,13 +1050,25 @@ hipError_t launch_decode_sk(const MqParams& p, int ncb, bool merge, hipStream_t 
     return hipErrorInvalidValue;
   const int64_t merge_wgs = ((int64_t)p.num_seqs * p.mq_max_q * p.Hq + 3) / 4;  // one wave per (row, head)
   if (merge_wgs > 0x7fffffff) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)p.sk_wgs), block((unsigned)(64 * hg));
+  // the work list of a prefill call: one more workgroup
+  PrefillParams ppv{};
+  PrefillItem* it = nullptr;
+  int n_items = 0;
+  if (items != nullptr) {
+    if (pp == nullptr || !varlen) return hipErrorInvalidValue;
+    const int64_t n_items_max = (int64_t)pp->num_seqs * pp->n_mblocks;
+    if (n_items_max > 0x7fffffff) return hipErrorInvalidValue;
+    ppv = *pp;
+    it = static_cast<PrefillItem*>(items);
+    n_items = (int)n_items_max;
+  }
+  const dim3 grid((unsigned)p.sk_wgs + (it != nullptr ? 1u : 0u)), block((unsigned)(64 * hg));
   switch (sk_variant(ncb, hg, p.G, varlen)) {
-    case 0: hipLaunchKernelGGL((decode_sk_kernel<1, 4, false>), grid, block, 0, stream, p); break;
-    case 1: hipLaunchKernelGGL((decode_sk_kernel<2, 4, false>), grid, block, 0, stream, p); break;
-    case 2: hipLaunchKernelGGL((decode_sk_kernel<1, 8, true>), grid, block, 0, stream, p); break;
-    case 3: hipLaunchKernelGGL((decode_sk_kernel<1, 8, false>), grid, block, 0, stream, p); break;
-    default: hipLaunchKernelGGL((decode_sk_kernel<2, 8, false>), grid, block, 0, stream, p); break;
+    case 0: hipLaunchKernelGGL((decode_sk_kernel<1, 4, false>), grid, block, 0, stream, p, ppv, it, n_items); break;
+    case 1: hipLaunchKernelGGL((decode_sk_kernel<2, 4, false>), grid, block, 0, stream, p, ppv, it, n_items); break;
+    case 2: hipLaunchKernelGGL((decode_sk_kernel<1, 8, true>), grid, block, 0, stream, p, ppv, it, n_items); break;
+    case 3: hipLaunchKernelGGL((decode_sk_kernel<1, 8, false>), grid, block, 0, stream, p, ppv, it, n_items); break;
+    default: hipLaunchKernelGGL((decode_sk_kernel<2, 8, false>), grid, block, 0, stream, p, ppv, it, n_items); break;
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;

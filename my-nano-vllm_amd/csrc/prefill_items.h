@@ -45,52 +45,64 @@ __device__ __forceinline__ bool item_valid(const PrefillParams& p, const ItemGeo
   return g.Lq > p.mq_max_q && mb * p.BM < g.Lq;
 }
 
-// Work list of the prefill kernel: one 256-thread workgroup writes the
+// Work list of the prefill kernel: one workgroup (256 threads or more; the
+// first 256 do the work, the rest only take part in the barriers) writes the
 // (seq, m-block) items in decreasing tile count (counting sort), followed by
 // records with seq = -1 for slots without an item.  Run as an extra
-// workgroup of the short-query launch that precedes the prefill kernel.
+// workgroup of the launch that precedes the prefill kernel.
 __device__ __forceinline__ void prefill_schedule(const PrefillParams& p, PrefillItem* __restrict__ items,
                                                  int n_items_max) {
   __shared__ int hist[kCostBuckets];
   __shared__ int warp_tot[4];
   const int tid = threadIdx.x;
-  for (int b = tid; b < kCostBuckets; b += 256) hist[b] = 0;
+  const bool worker = tid < 256;
+  const int lane = tid & 63, wave = tid >> 6;
+  if (worker)
+    for (int b = tid; b < kCostBuckets; b += 256) hist[b] = 0;
   __syncthreads();
-  for (int idx = tid; idx < n_items_max; idx += 256) {
-    const int seq = idx / p.n_mblocks, mb = idx - seq * p.n_mblocks;
-    const ItemGeom g = item_geom(p, seq);
-    if (!item_valid(p, g, mb)) continue;
-    atomicAdd(&hist[min(item_tiles(p, g, mb), kCostBuckets - 1)], 1);
-  }
+  if (worker)
+    for (int idx = tid; idx < n_items_max; idx += 256) {
+      const int seq = idx / p.n_mblocks, mb = idx - seq * p.n_mblocks;
+      const ItemGeom g = item_geom(p, seq);
+      if (!item_valid(p, g, mb)) continue;
+      atomicAdd(&hist[min(item_tiles(p, g, mb), kCostBuckets - 1)], 1);
+    }
   __syncthreads();
   // Exclusive scan in decreasing cost order: thread t owns buckets
   // [1023 - 4t - 3, 1023 - 4t] (walked from high cost to low).
-  int local[4], sum = 0;
+  int local[4] = {0, 0, 0, 0}, sum = 0, incl = 0;
+  if (worker) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    local[j] = hist[kCostBuckets - 1 - (4 * tid + j)];
-    sum += local[j];
-  }
-  int incl = sum;  // inclusive scan of per-thread sums over the wave
-  const int lane = tid & 63, wave = tid >> 6;
+    for (int j = 0; j < 4; ++j) {
+      local[j] = hist[kCostBuckets - 1 - (4 * tid + j)];
+      sum += local[j];
+    }
+    incl = sum;  // inclusive scan of per-thread sums over the wave
 #pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int o = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += o;
-  }
-  if (lane == 63) warp_tot[wave] = incl;
-  __syncthreads();
-  int base = 0;
-  for (int w = 0; w < wave; ++w) base += warp_tot[w];
-  const int total = warp_tot[0] + warp_tot[1] + warp_tot[2] + warp_tot[3];
-  int run = base + incl - sum;
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    hist[kCostBuckets - 1 - (4 * tid + j)] = run;
-    run += local[j];
+    for (int off = 1; off < 64; off <<= 1) {
+      const int o = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += o;
+    }
+    if (lane == 63) warp_tot[wave] = incl;
   }
   __syncthreads();
+  int total = 0, run = 0;
+  if (worker) {
+    int base = 0;
+    for (int w = 0; w < wave; ++w) base += warp_tot[w];
+    total = warp_tot[0] + warp_tot[1] + warp_tot[2] + warp_tot[3];
+    run = base + incl - sum;
+  }
+  __syncthreads();
+  if (worker) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      hist[kCostBuckets - 1 - (4 * tid + j)] = run;
+      run += local[j];
+    }
+  }
+  __syncthreads();
+  if (!worker) return;
   for (int idx = tid; idx < n_items_max; idx += 256) {
     const int seq = idx / p.n_mblocks, mb = idx - seq * p.n_mblocks;
     const ItemGeom g = item_geom(p, seq);
