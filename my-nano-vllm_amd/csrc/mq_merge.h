@@ -127,7 +127,21 @@ __device__ __forceinline__ void sk_merge_one(const MqParams& p, int b, int idx, 
   const int W = p.sk_wgs;
   const int64_t T = (int64_t)NHG * p.sk_prefix[p.num_seqs];
   const int64_t P = (int64_t)NHG * pre_b + (int64_t)hg * n;
-  const int wf = sk_owner(P, T, W), wl = sk_owner(P + n - 1, T, W);
+  // owners of the pair's first and last stages, and wf's slot (below); in
+  // 32-bit arithmetic when T * (W + 1) < 2^32 (every product below is then
+  // below 2^32), since a 64-bit division is a long instruction sequence and
+  // this pass runs one per wave
+  int wf, wl, slot_f;
+  if (T < (int64_t)(0xffffffffu / (uint32_t)(W + 1))) {
+    const uint32_t t = (uint32_t)T, uw = (uint32_t)W, p0 = (uint32_t)P;
+    wf = (int)(((p0 + 1u) * uw + t - 1u) / t) - 1;
+    wl = (int)(((p0 + (uint32_t)n) * uw + t - 1u) / t) - 1;
+    slot_f = ((uint32_t)wf * t / uw < p0) ? 1 : 0;
+  } else {
+    wf = sk_owner(P, T, W);
+    wl = sk_owner(P + n - 1, T, W);
+    slot_f = ((int64_t)wf * T / W < P) ? 1 : 0;
+  }
   if (wf == wl) return;  // finished by its workgroup
   // Workgroups in (wf, wl] start inside the pair, so it is their first pair
   // (slot 0); wf holds it in slot 0 if its range starts at P, else in slot 1
@@ -135,7 +149,6 @@ __device__ __forceinline__ void sk_merge_one(const MqParams& p, int b, int idx, 
   // with empty ranges wrote nothing and are skipped.  (64-bit divisions are
   // long instruction sequences: one per contributor made this pass
   // instruction-bound when pairs are cut many times.)
-  const int slot_f = ((int64_t)wf * T / W < P) ? 1 : 0;
   const bool may_be_empty = T < W;
   auto slot_ptr = [&](int w) -> const float* {
     if (may_be_empty && (int64_t)w * T / W == (int64_t)(w + 1) * T / W) return nullptr;
