@@ -23,7 +23,9 @@ Secondary fields in the same JSON line:
                512-token chunks, Qwen3-8B shapes), TFLOP/s, and its
                speculative rows alone, GB/s over their decode bytes;
   contiguous_prefill  the mixed batch's 1024-token contiguous-layout prompt
-               (block_tables=None), TFLOP/s.
+               (block_tables=None), TFLOP/s;
+  contiguous_prefill_batch  the prefill workload in the contiguous layout
+               (its K/V rows gathered per sequence), TFLOP/s.
 These are timed after 0.15 s of sustained warm-up calls (the shader clock
 settles lower under continuous MFMA load within the first tens of
 milliseconds); the headline decode field runs exactly --warmup warm-up calls.
@@ -58,6 +60,7 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "my-nano-vllm_amd"))
 
+import numpy as np  # noqa: E402
 import torch  # noqa: E402
 
 from nanovllm_amd import workloads as W  # noqa: E402
@@ -207,6 +210,32 @@ def bench_contiguous(n_tok, hq, hkv, steps, warmup):
     return dict(ms=ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12)
 
 
+def bench_contiguous_batch(wl, pools, q, steps, warmup):
+    """The workload's own sequences in the contiguous layout (block_tables=None):
+    each pool's K/V rows of every sequence gathered into [sum Lk, Hkv, 128]
+    tensors (one copy per pool, alternated), same queries, same flops."""
+    rows = np.concatenate([wl.slots_for(i, 0, s.lk) for i, s in enumerate(wl.seqs)]).astype(np.int64)
+    idx = torch.from_numpy(rows).cuda()
+    hkv = wl.num_kv_heads
+    conts = []
+    for kc, vc in pools:
+        conts.append(tuple(c.view(torch.uint8).reshape(-1, hkv, 128)[idx].view(torch.float8_e4m3fn)
+                           for c in (kc, vc)))
+    cu_q_np, _ = wl.cu_seqlens()
+    cu_q = torch.from_numpy(cu_q_np).cuda()
+    cu_k = torch.from_numpy(np.concatenate([[0], np.cumsum(wl.lk())]).astype(np.int32)).cuda()
+    max_q, max_k = int(wl.lq().max()), int(wl.lk().max())
+
+    def step(i):
+        k, v = conts[i % len(conts)]
+        fp8_prefill_attention(q, k, v, block_tables=None, cu_seqlens_q=cu_q, cu_seqlens_k=cu_k,
+                              max_seqlen_q=max_q, max_seqlen_k=max_k, softmax_scale=SCALE)
+
+    ms = timed(step, steps, warmup, SECONDARY_WARM_S)
+    flops = wl.attention_flops()
+    return dict(ms=ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12)
+
+
 def copy_probe(reps=4):
     """A plain device copy of known size: its FETCH_SIZE / WRITE_SIZE readings
     under rocprofv3 --pmc give the counters' scale."""
@@ -303,14 +332,22 @@ def main():
     if args.only in ("prefill", "all"):
         wl = W.qwen3_8b_prefill()
         log(f"prefill workload {wl.name}: flops={wl.attention_flops()}")
-        res, pools, _ = bench_prefill(wl, max(args.steps // 2, 5), max(args.warmup // 2, 2), warm_s=SECONDARY_WARM_S)
+        res, pools, q = bench_prefill(wl, max(args.steps // 2, 5), max(args.warmup // 2, 2), warm_s=SECONDARY_WARM_S)
         log(f"prefill: {res['ms'] * 1e3:.1f} us/step, {res['tflops']:.1f} TFLOP/s")
         extra["prefill"] = dict(workload=wl.name, ms_per_step=round(res["ms"], 5),
                                 tflops=round(res["tflops"], 2),
                                 frac_bf16_peak=round(res["tflops"] / BF16_PEAK_TFLOPS, 4),
                                 algorithmic_flops_per_step=res["flops"],
-                                kernels="prefill_short_kernel<2,2> (short-query rows, none here, and the work list) + varlen_prefill_kernel")
-        del pools
+                                kernels="decode_sk_kernel<2,8> (short-query rows, none here; one workgroup "
+                                        "writes the work list) + varlen_prefill_kernel<true>")
+        res_b = bench_contiguous_batch(wl, pools, q, max(args.steps // 2, 5), max(args.warmup // 2, 2))
+        log(f"prefill, contiguous layout: {res_b['ms'] * 1e3:.1f} us/step, {res_b['tflops']:.1f} TFLOP/s")
+        extra["contiguous_prefill_batch"] = dict(
+            workload=wl.name + " in the contiguous layout (block_tables=None, K/V gathered per sequence)",
+            ms_per_step=round(res_b["ms"], 5), tflops=round(res_b["tflops"], 2),
+            frac_bf16_peak=round(res_b["tflops"] / BF16_PEAK_TFLOPS, 4), algorithmic_flops_per_step=res_b["flops"],
+            kernels="prefill_short_kernel (the work list) + varlen_prefill_kernel<false>")
+        del pools, q
         torch.cuda.empty_cache()
 
     if args.only in ("store", "all"):
@@ -344,7 +381,9 @@ def main():
             spec_rows_only=dict(ms_per_step=round(res_s["ms"], 5), algorithmic_bytes_per_step=spec_bytes,
                                 gbs=round(spec_bytes / (res_s["ms"] * 1e-3) / 1e9, 2),
                                 frac_hbm_peak=round(spec_bytes / (res_s["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)),
-            kernels="prefill_short_kernel (speculative rows, split-KV) + varlen_prefill_kernel (chunks, and the merge)")
+            kernels="decode_sk_kernel<2,8> (speculative rows, stream-K; one workgroup writes the work list) + "
+                    "varlen_prefill_kernel<true> (chunks, and the merge); speculative rows alone: decode_sk_kernel "
+                    "+ decode_sk_merge_kernel")
         extra["contiguous_prefill"] = dict(
             workload="qwen3_8b_mixed contiguous prompt: 1024 tokens, block_tables=None (32/8 heads)",
             ms_per_step=round(res_c["ms"], 5), tflops=round(res_c["tflops"], 2),
