@@ -28,7 +28,7 @@ struct MqParams {
   int mq_max_q;                 // varlen mode: only sequences with 1 <= Lq <= mq_max_q
   float scale_log2;
   // Balanced decode (stream-K over KV stages), see decode_sk_kernel.
-  float* sk_part;               // [sk_wgs, 2, sk_heads, sk_cols, kSkSlotFloats] partial (acc, m, l)
+  float* sk_part;               // [sk_wgs, 2, sk_heads, sk_cols, kSkSlotFloats] partials (see kSkSlotFloats)
   int32_t* sk_prefix;           // [num_seqs + 1] stages per kv-head group before each sequence
   int sk_wgs;                   // persistent workgroups
   int sk_heads;                 // kv heads per workgroup (4 or 8; one wave each)
@@ -37,7 +37,11 @@ struct MqParams {
 
 // Balanced decode: 16-token stages.
 constexpr int kSkStageTokens = 16;
-constexpr int kSkSlotFloats = 132;  // acc[128], m, l, 2 pad
+// A cut pair's partial per query column: acc / l as fp16[128] (a weighted
+// mean of V rows, |.| <= 448, so fp16 holds it to 2^-11 relative; the
+// output is rounded to fp16 anyway), then m and l as fp32, 2 pad: 68 floats.
+constexpr int kSkSlotFloats = 68;
+constexpr int kSkSlotMl = 64;  // float offset of (m, l) in a slot
 constexpr int kSkMaxSeqs = 6136;    // the stage prefix and lengths (2 * num_seqs + 1 ints) fit the 48 KiB LDS ring
 
 // Waves per prefill workgroup: each owns 32 query rows of one head.

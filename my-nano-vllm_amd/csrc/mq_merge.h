@@ -162,16 +162,16 @@ __device__ __forceinline__ void sk_merge_one(const MqParams& p, int b, int idx, 
   for (int w0 = wf; w0 <= wl; w0 += 8) {
     const int cnt = min(8, wl - w0 + 1);
     float mi = -INFINITY, li = 0.f;
-    f32x2 a[8];
+    uint32_t a[8];  // dims 2 lane, 2 lane + 1 of contributor j's acc / l (fp16)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      a[j] = f32x2{0.f, 0.f};
+      a[j] = 0u;
       const float* ps = (j < cnt) ? slot_ptr(w0 + j) : nullptr;
       if (ps != nullptr) {
-        a[j] = *reinterpret_cast<const f32x2*>(ps + 2 * lane);
+        a[j] = reinterpret_cast<const uint32_t*>(ps)[lane];
         if (lane == j) {
-          mi = ps[kHeadDim];
-          li = ps[kHeadDim + 1];
+          mi = ps[kSkSlotMl];
+          li = ps[kSkSlotMl + 1];
         }
       }
     }
@@ -192,10 +192,11 @@ __device__ __forceinline__ void sk_merge_one(const MqParams& p, int b, int idx, 
     for (int off = 4; off > 0; off >>= 1) lw += shfl_xor_f32(lw, off);
     Lsum += __shfl(lw, 0, 64);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float wk = __shfl(wi, j, 64);
-      o0 += wk * a[j].x;
-      o1 += wk * a[j].y;
+    for (int j = 0; j < 8; ++j) {  // weight of a normalised partial: w_j * l_j
+      const float wk = __shfl(li * wi, j, 64);
+      const f16x2 h = __builtin_bit_cast(f16x2, a[j]);
+      o0 += wk * (float)h.x;
+      o1 += wk * (float)h.y;
     }
   }
   const float inv = (Lsum > 0.f) ? 1.0f / Lsum : 0.f;

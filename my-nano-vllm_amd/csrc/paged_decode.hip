@@ -946,16 +946,19 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p, PrefillP
       } else {
         const int slot = first_seg ? 0 : 1;
         float* ps = p.sk_part + ((((int64_t)w * 2 + slot) * HG + wave) * p.sk_cols + col) * kSkSlotFloats;
+        const float inv = (lsum[cb] > 0.f) ? 1.0f / lsum[cb] : 0.f;  // normalised: fp16 holds it
+        uint16_t* ph = reinterpret_cast<uint16_t*>(ps);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          *reinterpret_cast<f32x4*>(ps + 32 * gam + 8 * k) =
-              f32x4{acc[cb][0][k], acc[cb][1][k], acc[cb][2][k], acc[cb][3][k]};
-          *reinterpret_cast<f32x4*>(ps + 32 * gam + 8 * k + 4) =
-              f32x4{acc[cb][4][k], acc[cb][5][k], acc[cb][6][k], acc[cb][7][k]};
+          const u32x4 h8 = {pack_f16x2(acc[cb][0][k] * inv, acc[cb][1][k] * inv),
+                            pack_f16x2(acc[cb][2][k] * inv, acc[cb][3][k] * inv),
+                            pack_f16x2(acc[cb][4][k] * inv, acc[cb][5][k] * inv),
+                            pack_f16x2(acc[cb][6][k] * inv, acc[cb][7][k] * inv)};
+          *reinterpret_cast<u32x4*>(ph + 32 * gam + 8 * k) = h8;
         }
         if (gam == 0) {
-          ps[kHeadDim] = m[cb];
-          ps[kHeadDim + 1] = lsum[cb];
+          ps[kSkSlotMl] = m[cb];
+          ps[kSkSlotMl + 1] = lsum[cb];
         }
       }
     }
