@@ -148,13 +148,11 @@ __device__ __forceinline__ void sk_merge_one(const MqParams& p, int b, int idx, 
   // (its last pair).  With T >= W no range is empty; otherwise workgroups
   // with empty ranges wrote nothing and are skipped.  (64-bit divisions are
   // long instruction sequences: one per contributor made this pass
-  // instruction-bound when pairs are cut many times.)
+  // instruction-bound when pairs are cut many times.)  Slot s of workgroup w
+  // for (hh, col) is at base + (2w + s) * wstride.
   const bool may_be_empty = T < W;
-  auto slot_ptr = [&](int w) -> const float* {
-    if (may_be_empty && (int64_t)w * T / W == (int64_t)(w + 1) * T / W) return nullptr;
-    const int slot = (w == wf) ? slot_f : 0;
-    return p.sk_part + ((((int64_t)w * 2 + slot) * HG + hh) * p.sk_cols + col) * kSkSlotFloats;
-  };
+  const float* base = p.sk_part + (int64_t)(hh * p.sk_cols + col) * kSkSlotFloats;
+  const int64_t wstride = (int64_t)HG * p.sk_cols * kSkSlotFloats;
   // Contributors in chunks of 8: all of a chunk's loads (lane j < 8 reads
   // (m, l) of contributor j, every lane its 2 dims of each) are issued
   // before any is used, so a chunk costs one memory round trip.
@@ -162,12 +160,19 @@ __device__ __forceinline__ void sk_merge_one(const MqParams& p, int b, int idx, 
   for (int w0 = wf; w0 <= wl; w0 += 8) {
     const int cnt = min(8, wl - w0 + 1);
     float mi = -INFINITY, li = 0.f;
+    uint32_t skip = 0;  // bit j: contributor j has an empty range (only when T < W)
+    if (may_be_empty) {
+#pragma nounroll
+      for (int j = 0; j < cnt; ++j)
+        if ((int64_t)(w0 + j) * T / W == (int64_t)(w0 + j + 1) * T / W) skip |= 1u << j;
+    }
     uint32_t a[8];  // dims 2 lane, 2 lane + 1 of contributor j's acc / l (fp16)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       a[j] = 0u;
-      const float* ps = (j < cnt) ? slot_ptr(w0 + j) : nullptr;
-      if (ps != nullptr) {
+      if (j < cnt && !((skip >> j) & 1u)) {
+        const int w = w0 + j;
+        const float* ps = base + (int64_t)(2 * w + (w == wf ? slot_f : 0)) * wstride;
         a[j] = reinterpret_cast<const uint32_t*>(ps)[lane];
         if (lane == j) {
           mi = ps[kSkSlotMl];

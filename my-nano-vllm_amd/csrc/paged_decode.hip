@@ -1003,11 +1003,12 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p, PrefillP
 // its mq_max_q * Hq (row, head) pairs); decode has one row per sequence
 // (mq_max_q = 1).
 __global__ __launch_bounds__(256) void decode_sk_merge_kernel(MqParams p) {
-  const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  // 32-bit indices: the launch checks num_seqs * mq_max_q * Hq < 2^31
+  const int gw = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
   const int per_seq = p.mq_max_q * p.Hq;
-  if (gw >= (int64_t)p.num_seqs * per_seq) return;
-  const int b = (int)(gw / per_seq);
-  sk_merge_one(p, b, (int)(gw - (int64_t)b * per_seq), threadIdx.x & 63);
+  if (gw >= p.num_seqs * per_seq) return;
+  const int b = gw / per_seq;
+  sk_merge_one(p, b, gw - b * per_seq, threadIdx.x & 63);
 }
 
 namespace {
@@ -1051,8 +1052,9 @@ hipError_t launch_decode_sk(const MqParams& p, int ncb, bool merge, const Prefil
       (ncb != 1 && ncb != 2) || p.mq_max_q < 1 || p.G * p.mq_max_q > 16 * ncb || p.sk_cols < p.G * p.mq_max_q ||
       (varlen && p.cu_k == nullptr) || (!varlen && (p.mq_max_q != 1 || p.context_lens == nullptr)))
     return hipErrorInvalidValue;
-  const int64_t merge_wgs = ((int64_t)p.num_seqs * p.mq_max_q * p.Hq + 3) / 4;  // one wave per (row, head)
-  if (merge_wgs > 0x7fffffff) return hipErrorInvalidValue;
+  const int64_t merge_waves = (int64_t)p.num_seqs * p.mq_max_q * p.Hq;  // one per (row, head)
+  if (merge_waves + 3 > 0x7fffffff) return hipErrorInvalidValue;
+  const int64_t merge_wgs = (merge_waves + 3) / 4;
   // the work list of a prefill call: one more workgroup
   PrefillParams ppv{};
   PrefillItem* it = nullptr;
