@@ -721,7 +721,16 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p, PrefillP
   const int64_t T = (int64_t)NHG * carry;
   if (w == 0)
     for (int b = tid; b <= B; b += kThreads) p.sk_prefix[b] = pre[b];
-  const int64_t start = (int64_t)w * T / W, end = (int64_t)(w + 1) * T / W;
+  // the range [w*T/W, (w+1)*T/W): in 32-bit arithmetic when (W+1)*T < 2^32
+  // (a 64-bit division is a long instruction sequence on the prologue's path)
+  int64_t start, end;
+  if (T < (int64_t)(0xffffffffu / (uint32_t)(W + 1))) {
+    start = (uint32_t)w * (uint32_t)T / (uint32_t)W;
+    end = (uint32_t)(w + 1) * (uint32_t)T / (uint32_t)W;
+  } else {
+    start = (int64_t)w * T / W;
+    end = (int64_t)(w + 1) * T / W;
+  }
   if (start >= end) return;
   // first pair: the last sequence b0 with NHG * pre[b0] <= start
   int lo = 0, hi = B - 1;
@@ -733,7 +742,8 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p, PrefillP
   const int b0 = lo;
   const int n0 = pre[b0 + 1] - pre[b0];
   const int64_t rem = start - (int64_t)NHG * pre[b0];
-  const int hg0 = (int)(rem / n0), o0 = (int)(rem - (int64_t)hg0 * n0);
+  const int hg0 = (rem >> 32) == 0 ? (int)((uint32_t)rem / (uint32_t)n0) : (int)(rem / n0);
+  const int o0 = (int)(rem - (int64_t)hg0 * n0);
   const int n_w = (int)(end - start);
   const int L0 = lens[b0];
   // varlen: the first pair's query rows, read here so that the read overlaps
