@@ -1,20 +1,25 @@
 """Benchmark of the MI355X FP8 paged-attention hot path (one GPU).
 
-Headline (``value``): FP8 paged decode at Qwen3-0.6B attention shapes (16
-query / 8 kv heads, head_dim 128, block 256, B = 256 sequences, context
-U[100, 2048], seeded), as achieved HBM GB/s over the algorithmic bytes of a
-step: each FP8 K/V byte once + bf16 Q in and O out + the block-table row and
-context length of every sequence.  One decode call is two launches: the
-balanced stream-K pass (``decode_sk_kernel<1,8,QL>``, one persistent
-workgroup per CU streaming an equal share of the KV stages) and the merge
-pass for sequences cut between workgroups (``decode_sk_merge_kernel``).  The
-HIP-event time of a call covers both, so ``roofline.achieved`` is the
-algorithmic bytes over the two launches together.
+Headline (``value``): FP8 paged decode at Qwen3-8B attention shapes -- the
+mixed batch's 192 plain-decode sequences on their own (32 query / 8 kv heads,
+head_dim 128, block 256, one query token each, context U[256, 4096], seeded,
+over the mixed batch's paged pool) -- as achieved HBM GB/s over the
+algorithmic bytes of a step: each FP8 K/V byte once + bf16 Q in and O out +
+the block-table row and context length of every sequence.  One decode call
+is two launches: the balanced stream-K pass (``decode_sk_kernel<1,8,QL>``,
+one persistent workgroup per CU streaming an equal share of the KV stages)
+and the merge pass for sequences cut between workgroups
+(``decode_sk_merge_kernel``).  The HIP-event time of a call covers both, so
+``roofline.achieved`` is the algorithmic bytes over the two launches
+together (a lower bound on the stream-K kernel's own rate).
 
 Secondary fields in the same JSON line:
+  decode_qwen3_0p6b  decode at Qwen3-0.6B shapes (16/8 heads, B = 256,
+               context U[100, 2048]), GB/s;
   prefill      varlen chunked prefill at Qwen3-8B shapes (32/8 heads, 16 x
                512-token chunks over cached context U[0, 4096]) in TFLOP/s of
-               unmasked causal pairs, vs the bf16 dense MFMA peak;
+               unmasked causal pairs, vs the bf16 dense MFMA peak, with its
+               own CPU baseline;
   long_decode  long-context decode at Qwen3-32B shapes (64/8 heads, B = 32,
                context U[32K, 128K], 1% of K/V x20);
   store        the KV store/quantise of the prefill workload's 8192 new
@@ -37,17 +42,17 @@ measured with HIP events recorded on the stream the kernels are launched on
 (torch's current stream).
 
 ``roofline.traffic`` comes from the committed rocprofv3 counter summary
-(profiles/decode_qwen3_0p6b_b256_pmc.json: FETCH_SIZE / WRITE_SIZE of the
-decode kernel, each scaled by the same counter's reading for a plain copy
+(profiles/decode_qwen3_8b_b192_pmc.json: FETCH_SIZE / WRITE_SIZE of the
+decode kernels, each scaled by the same counter's reading for a plain copy
 of known size, which ``--copy-probe`` runs); it is null if that file is
 absent.
 
 ``cpu_baseline`` times the oracle (torch-CPU dequant + fp32 attention, the
 parity tests' checker) on the host cores for a bounded sample of the same
-workload.
+workload; the prefill field carries one of its own.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--only decode|prefill|long|store|mixed|all] [--no-cpu-baseline]
+                    [--only decode|decode06|prefill|long|store|mixed|all] [--no-cpu-baseline]
                     [--copy-probe]
 """
 import argparse
@@ -59,11 +64,12 @@ import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "my-nano-vllm_amd"))
+sys.path.insert(0, os.path.join(ROOT, "tests"))  # seeded workloads (shared with the parity tests)
 
 import numpy as np  # noqa: E402
 import torch  # noqa: E402
 
-from nanovllm_amd import workloads as W  # noqa: E402
+import workloads as W  # noqa: E402
 from nanovllm_amd.kernels.fp8_attention import fp8_decode_attention, fp8_prefill_attention  # noqa: E402
 from nanovllm_amd.layers.attention import store_kvcache  # noqa: E402
 
@@ -71,7 +77,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 SCALE = 128 ** -0.5
 METRIC = "decode attn HBM GB/s (%peak) + prefill attn TFLOP/s, Qwen3-8B shapes, FP8 KV"
-PMC_SUMMARY = os.path.join(ROOT, "profiles", "decode_qwen3_0p6b_b256_pmc.json")
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "decode_qwen3_8b_b192_pmc.json")
 COPY_PROBE_BYTES = 1 << 30
 # The secondary fields (prefill, store, mixed, long decode) are timed after this much
 # sustained warm-up: under continuous MFMA load the shader clock drops over
@@ -85,7 +91,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="all", choices=["decode", "prefill", "long", "store", "mixed", "all"])
+    ap.add_argument("--only", default="all", choices=["decode", "decode06", "prefill", "long", "store", "mixed", "all"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 1 GiB device copy (counter scale for rocprofv3 --pmc)")
@@ -273,6 +279,37 @@ def cpu_baseline_decode(wl, pool, q, target_s=12.0):
                        f"({sum(times):.1f}s total); cpu={_cpu_model()}")
 
 
+def cpu_baseline_prefill(wl, pool, q, seqs=(0, 1), target_s=12.0):
+    """The oracle's varlen prefill on a bounded sample of the prefill workload:
+    the sequences ``seqs`` (their query rows and paged keys), repeated until
+    about `target_s` seconds of CPU work; the rate is the sample's unmasked
+    causal flops over the median pass."""
+    from oracle import attention as oa
+    sub = W.sub_workload(wl, list(seqs))
+    kc = pool[0].view(torch.uint8).cpu()
+    vc = pool[1].view(torch.uint8).cpu()
+    cu_q_full, _ = wl.cu_seqlens()
+    rows = np.concatenate([np.arange(cu_q_full[i], cu_q_full[i + 1]) for i in seqs])
+    qc = q[torch.from_numpy(rows).cuda()].cpu()
+    cu_q, cu_k = (torch.from_numpy(x) for x in sub.cu_seqlens())
+    bt = torch.from_numpy(sub.block_tables)
+    torch.set_num_threads(os.cpu_count() or 1)
+    oa.prefill_attention(qc, kc, vc, bt, cu_q, cu_k, SCALE)  # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while time.perf_counter() - t_start < target_s or len(times) < 3:
+        t0 = time.perf_counter()
+        oa.prefill_attention(qc, kc, vc, bt, cu_q, cu_k, SCALE)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    flops = sub.attention_flops()
+    desc = ", ".join(f"seq {i}: {wl.seqs[i].lq} rows over {wl.seqs[i].lk} keys" for i in seqs)
+    return dict(value=round(flops / t / 1e12, 5), unit="TFLOP/s", cores=torch.get_num_threads(), kind="port",
+                sample=f"{len(seqs)} of {wl.num_seqs} sequences of {wl.name} ({desc}; {flops / 1e9:.2f} GFLOP "
+                       f"of the call's {wl.attention_flops() / 1e9:.1f}) per pass, median of {len(times)} passes "
+                       f"of {t:.3f}s ({sum(times):.1f}s total); cpu={_cpu_model()}")
+
+
 def _cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -310,7 +347,7 @@ def main():
         copy_probe()
 
     if args.only in ("decode", "all"):
-        wl = W.qwen3_0p6b_decode()
+        wl = W.qwen3_8b_decode()
         log(f"decode workload {wl.name}: B={wl.num_seqs} bytes={wl.decode_bytes()}")
         res, pools, q = bench_decode(wl, args.steps, args.warmup)
         log(f"decode: {res['ms'] * 1e3:.1f} us/step, {res['gbs']:.1f} GB/s")
@@ -318,14 +355,29 @@ def main():
                     ms_per_step=round(res["ms"], 5),
                     roofline=dict(bound="hbm", achieved=round(res["gbs"], 2), peak=HBM_PEAK_GBS,
                                   unit="GB/s", frac=round(res["gbs"] / HBM_PEAK_GBS, 4),
-                                  traffic=_traffic_from_profile(), kernel="decode_sk_kernel<1,8,QL> + decode_sk_merge_kernel",
+                                  traffic=_traffic_from_profile(),
+                                  kernel="decode_sk_kernel<1,8,QL> + decode_sk_merge_kernel (one decode call)",
                                   algorithmic_bytes_per_launch=res["bytes"]),
                     config=dict(workload=wl.name, batch=wl.num_seqs, num_heads=wl.num_heads,
                                 num_kv_heads=wl.num_kv_heads, head_dim=128, block_size=wl.block_size,
-                                context="uniform[100,2048]", kv_dtype="float8_e4m3fn", kv_pools=2))
+                                context="uniform[256,4096] (the mixed batch's plain-decode rows)",
+                                kv_dtype="float8_e4m3fn", kv_pools=2))
         if not args.no_cpu_baseline:
             log("cpu baseline (oracle) on the decode workload")
             line["cpu_baseline"] = cpu_baseline_decode(wl, pools[0], q)
+        del pools
+        torch.cuda.empty_cache()
+
+    if args.only in ("decode06", "all"):
+        wl = W.qwen3_0p6b_decode()
+        log(f"decode workload {wl.name}: B={wl.num_seqs} bytes={wl.decode_bytes()}")
+        res, pools, q = bench_decode(wl, args.steps, args.warmup)
+        log(f"decode (0.6B shapes): {res['ms'] * 1e3:.1f} us/step, {res['gbs']:.1f} GB/s")
+        extra["decode_qwen3_0p6b"] = dict(workload=wl.name + " (16/8 heads, B=256, ctx U[100, 2048])",
+                                          ms_per_step=round(res["ms"], 5), gbs=round(res["gbs"], 2),
+                                          frac_hbm_peak=round(res["gbs"] / HBM_PEAK_GBS, 4),
+                                          algorithmic_bytes_per_step=res["bytes"],
+                                          kernels="decode_sk_kernel<1,8,QL> + decode_sk_merge_kernel")
         del pools
         torch.cuda.empty_cache()
 
@@ -340,6 +392,9 @@ def main():
                                 algorithmic_flops_per_step=res["flops"],
                                 kernels="decode_sk_kernel<2,8> (short-query rows, none here; one workgroup "
                                         "writes the work list) + varlen_prefill_kernel<true>")
+        if not args.no_cpu_baseline:
+            log("cpu baseline (oracle) on a sample of the prefill workload")
+            extra["prefill"]["cpu_baseline"] = cpu_baseline_prefill(wl, pools[0], q)
         res_b = bench_contiguous_batch(wl, pools, q, max(args.steps // 2, 5), max(args.warmup // 2, 2))
         log(f"prefill, contiguous layout: {res_b['ms'] * 1e3:.1f} us/step, {res_b['tflops']:.1f} TFLOP/s")
         extra["contiguous_prefill_batch"] = dict(

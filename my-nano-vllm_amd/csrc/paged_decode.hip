@@ -12,9 +12,12 @@
 //
 // Per 16-token chunk a wave computes, in fp32 accumulators:
 //     S^T[token][col] = K[token][:] . Q[col][:]      4 x v_mfma_f32_16x16x32_bf16 per column block
-//     O^T[dim][col]  += V^T[dim][token] . P^T[token][col]   8 x v_mfma_f32_16x16x16_bf16
-// The FP8 cache bytes are converted to bf16 exactly with
-// v_cvt_scalef32_pk_bf16_fp8 (scale 1.0).
+//     O^T[dim][col]  += V^T[dim][token] . P^T[token][col]   8 x v_mfma_f32_16x16x16_f16
+// The FP8 cache bytes are converted exactly, K to bf16 and V to fp16, with
+// v_cvt_scalef32_pk_{bf16,f16}_fp8 (scale 1.0).  The softmax weights P are
+// rounded to fp16 (11-bit significand; the lazy rescale keeps them below
+// 2^8), and the row sum adds those rounded weights, so numerator and
+// denominator use the same P.
 //
 // Lane layouts (lane = 16*gam + r, gam in 0..3, r in 0..15):
 //   K operand : lane loads 2x16 B of token row r, bytes [16gam + 64h, +16);
@@ -72,9 +75,16 @@ __device__ __forceinline__ bf16x8 fp8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
                    fp8x2_to_bf16x2<false>(hi), fp8x2_to_bf16x2<true>(hi));
 }
 
-__device__ __forceinline__ s16x4 as_s16x4(uint32_t a, uint32_t b) {
+__device__ __forceinline__ f16x4 as_f16x4(uint32_t a, uint32_t b) {
   u32x2 t = {a, b};
-  return __builtin_bit_cast(s16x4, t);
+  return __builtin_bit_cast(f16x4, t);
+}
+
+// Two E4M3FN bytes held in the low (HI=false) or high (HI=true) 16 bits of w
+// -> two fp16 packed in one dword.  Exact.
+template <bool HI>
+__device__ __forceinline__ uint32_t fp8x2_to_f16x2(uint32_t w) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, HI));
 }
 
 // max over the 4 lanes {l, l^16, l^32, l^48} (the lane groups holding one
@@ -117,8 +127,8 @@ __device__ __forceinline__ void attend_chunk(const ChunkRegs& cr, const bf16x8 (
     s[cb] = a;
   }
 
-  // ---- V^T operands: byte transpose of the 4 token rows --------------------
-  s16x4 vop[8];
+  // ---- V^T operands: byte transpose of the 4 token rows, exact fp16 ---------
+  f16x4 vop[8];
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
     const uint32_t x0 = half ? cr.v[0].y : cr.v[0].x;
@@ -129,10 +139,10 @@ __device__ __forceinline__ void attend_chunk(const ChunkRegs& cr, const bf16x8 (
     const uint32_t b01 = __builtin_amdgcn_perm(x0, x1, 0x03070206u);  // [t0d2 t1d2 t0d3 t1d3]
     const uint32_t a23 = __builtin_amdgcn_perm(x2, x3, 0x01050004u);
     const uint32_t b23 = __builtin_amdgcn_perm(x2, x3, 0x03070206u);
-    vop[4 * half + 0] = as_s16x4(fp8x2_to_bf16x2<false>(a01), fp8x2_to_bf16x2<false>(a23));
-    vop[4 * half + 1] = as_s16x4(fp8x2_to_bf16x2<true>(a01), fp8x2_to_bf16x2<true>(a23));
-    vop[4 * half + 2] = as_s16x4(fp8x2_to_bf16x2<false>(b01), fp8x2_to_bf16x2<false>(b23));
-    vop[4 * half + 3] = as_s16x4(fp8x2_to_bf16x2<true>(b01), fp8x2_to_bf16x2<true>(b23));
+    vop[4 * half + 0] = as_f16x4(fp8x2_to_f16x2<false>(a01), fp8x2_to_f16x2<false>(a23));
+    vop[4 * half + 1] = as_f16x4(fp8x2_to_f16x2<true>(a01), fp8x2_to_f16x2<true>(a23));
+    vop[4 * half + 2] = as_f16x4(fp8x2_to_f16x2<false>(b01), fp8x2_to_f16x2<false>(b23));
+    vop[4 * half + 3] = as_f16x4(fp8x2_to_f16x2<true>(b01), fp8x2_to_f16x2<true>(b23));
   }
 
   // ---- online softmax + O^T += V^T . P^T -----------------------------------
@@ -160,11 +170,15 @@ __device__ __forceinline__ void attend_chunk(const ChunkRegs& cr, const bf16x8 (
     const float m_use = (m[cb] == -INFINITY) ? 0.f : m[cb];
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = fast_exp2(v[i] - m_use);
-    lsum[cb] += (v[0] + v[1]) + (v[2] + v[3]);
-    const s16x4 pop = as_s16x4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+    const uint32_t p01 = pack_f16x2(v[0], v[1]), p23 = pack_f16x2(v[2], v[3]);
+    // row sum of the fp16 weights the MFMAs use (v_dot2_f32_f16 against 1.0, 1.0)
+    const f16x2 ones = __builtin_bit_cast(f16x2, 0x3c003c00u);
+    lsum[cb] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p01), ones, lsum[cb], false);
+    lsum[cb] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p23), ones, lsum[cb], false);
+    const f16x4 pop = as_f16x4(p01, p23);
 #pragma unroll
     for (int i = 0; i < 8; ++i)
-      acc[cb][i] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vop[i], pop, acc[cb][i], 0, 0, 0);
+      acc[cb][i] = __builtin_amdgcn_mfma_f32_16x16x16f16(vop[i], pop, acc[cb][i], 0, 0, 0);
   }
 }
 

@@ -1,11 +1,11 @@
 """MI355X-native FP8 paged-attention hot path for nano-vLLM.
 
-Public surface (drop-in for the reference's modules of the same names):
+Public surface (drop-in for the reference's functions of the same names):
   nanovllm_amd.kernels.fp8_attention: fp8_decode_attention, fp8_prefill_attention
-  nanovllm_amd.layers.attention:      store_kvcache, Attention
+  nanovllm_amd.layers.attention:      store_kvcache
   nanovllm_amd.utils.context:         Context, get_context, set_context, reset_context
   nanovllm_amd.engine.metadata:       host-side slot mapping / cu_seqlens / block tables
   nanovllm_amd.engine.graph:          pure-decode HIP-graph capture and replay
 """
 from .kernels.fp8_attention import fp8_decode_attention, fp8_prefill_attention  # noqa: F401
-from .layers.attention import Attention, store_kvcache  # noqa: F401
+from .layers.attention import store_kvcache  # noqa: F401

@@ -1,1 +1,1 @@
-"""Attention layer and FP8 KV store."""
+"""FP8 KV store (drop-in for store_kvcache)."""

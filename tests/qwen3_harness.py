@@ -4,7 +4,7 @@ A minimal Qwen3 decoder (the layer structure of nanovllm/models/qwen3.py:
 q/k RMSNorm per head, neox RoPE, GQA attention, SiLU-gated MLP, pre-norm
 residual blocks, final norm, LM head) whose attention is either
 
-* ``nanovllm_amd.layers.attention.Attention`` -- the product path: FP8 KV
+* ``attention_layer.Attention`` (the reference layer over the product path): FP8 KV
   store + HIP decode / prefill kernels on the GPU, or
 * ``OracleAttention`` -- the same layer contract computed by the oracle on
   the CPU (oracle store into CPU caches, oracle decode / prefill).
@@ -23,7 +23,7 @@ import torch
 from torch import nn
 
 from nanovllm_amd.engine.metadata import prepare_sequence
-from nanovllm_amd.layers.attention import Attention
+from attention_layer import Attention
 from nanovllm_amd.utils.context import get_context, reset_context
 from oracle import attention as oa
 from oracle import fp8 as ofp8

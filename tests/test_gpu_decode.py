@@ -7,8 +7,9 @@ from gpu_util import announce, assert_close, build_pair
 from oracle import attention as oa
 from oracle import fp8 as ofp8
 from nanovllm_amd import _native
-from nanovllm_amd import workloads as W
+import workloads as W
 from nanovllm_amd.kernels.fp8_attention import fp8_decode_attention
+from nanovllm_amd.layers.attention import store_kvcache
 
 pytestmark = pytest.mark.gpu
 SCALE = 128 ** -0.5
@@ -27,11 +28,14 @@ def _oracle_decode(wl, cpu_caches, q_cpu):
                                torch.from_numpy(wl.context_lens()), SCALE)
 
 
-@pytest.mark.parametrize("make", [W.tiny_decode, W.qwen3_0p6b_decode])
+@pytest.mark.parametrize("make", [W.tiny_decode, W.qwen3_0p6b_decode, W.qwen3_8b_decode])
 def test_decode_matches_oracle(make):
+    """The small CPU case, the Qwen3-0.6B decode batch (B = 256, 16/8 heads) and
+    the mixed batch's 192 plain-decode rows at Qwen3-8B shapes (32/8 heads, ctx
+    U[256, 4096]), all rows and heads against the oracle."""
     wl = make()
     announce(f"decode: {wl.name}")
-    cpu_c, gpu_c = build_pair(wl)
+    cpu_c, gpu_c = build_pair(wl, gen_device="cuda")
     q = wl.make_q("cpu")
     out = _run_decode(wl, gpu_c, q.cuda())
     assert_close(out, _oracle_decode(wl, cpu_c, q), wl.name)
@@ -123,7 +127,6 @@ def test_decode_long_context_big_pool():
     from gpu_util import cpu_store
     small.fill_cache(kc_cpu, vc_cpu, cpu_store)
     kc_gpu, vc_gpu = big.empty_caches("cuda")
-    from nanovllm_amd.layers.attention import store_kvcache
     big.fill_cache(kc_gpu, vc_gpu, store_kvcache)
     q = big.make_q("cpu")
     out = _run_decode(big, (kc_gpu, vc_gpu), q.cuda())
@@ -179,3 +182,30 @@ def test_decode_outlier_kv(ctx_lo, ctx_hi):
     want = _oracle_decode(wl, cpu_c, q)
     assert_close(_run_decode(wl, gpu_c, q.cuda()), want, "balanced decode, outliers")
     assert_close(_forced_split_decode(wl, gpu_c, q.cuda(), 256), want, "split-KV decode, outliers")
+
+
+def test_decode_long_context_outliers_full_size():
+    """The long-decode workload at full size: B = 32, 64/8 heads, ctx U[32K, 128K]
+    (up to 130,832 keys), 1 % of the K/V entries x20 before quantisation, a
+    pool of 13,673 blocks (past the reference's int32 offsets).  Every row of
+    the balanced (stream-K) kernel is compared with the split-KV kernel
+    (15,872-token partitions) on the same cache, and the shortest sequence,
+    the longest and two more (all 64 heads) with the oracle on the same cache
+    bytes (the blocks they use copied to the host)."""
+    wl = W.qwen3_32b_long_decode()
+    announce(f"decode: {wl.name} full size, B={wl.num_seqs}, max ctx {int(wl.context_lens().max())}")
+    kc, vc = wl.empty_caches("cuda")
+    wl.fill_cache(kc, vc, store_kvcache, gen_device="cuda")
+    q = wl.make_q("cuda")
+    bal = _run_decode(wl, (kc, vc), q)
+    split = _forced_split_decode(wl, (kc, vc), q, 15872)
+    assert_close(bal, split, "long decode: balanced vs split-KV")
+    ctx = wl.context_lens()
+    pick = sorted({int(ctx.argmin()), int(ctx.argmax()), 7, 19})
+    sub = W.sub_workload(wl, pick, compact=True)
+    bt = wl.block_tables[pick]
+    used = torch.from_numpy(np.unique(bt[bt >= 0]).astype(np.int64)).cuda()
+    kc_s, vc_s = kc[used].cpu(), vc[used].cpu()
+    want = oa.decode_attention(q[pick].cpu(), kc_s, vc_s, torch.from_numpy(sub.block_tables),
+                               torch.from_numpy(sub.context_lens()), SCALE)
+    assert_close(bal[pick], want, f"long decode: sequences {pick} vs oracle")

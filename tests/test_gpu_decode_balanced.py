@@ -11,7 +11,7 @@ import torch
 from gpu_util import announce, assert_close, build_pair
 from oracle import attention as oa
 from nanovllm_amd import _native
-from nanovllm_amd import workloads as W
+import workloads as W
 from nanovllm_amd.kernels.fp8_attention import fp8_decode_attention
 
 pytestmark = pytest.mark.gpu

@@ -5,9 +5,9 @@ import pytest
 import torch
 
 from gpu_util import announce
-from nanovllm_amd import workloads as W
+import workloads as W
 from nanovllm_amd.engine.graph import DecodeGraphRunner
-from nanovllm_amd.layers.attention import Attention
+from attention_layer import Attention
 from nanovllm_amd.utils.context import get_context, reset_context, set_context
 
 pytestmark = pytest.mark.gpu

@@ -5,7 +5,7 @@ import torch
 
 from gpu_util import announce, assert_close, build_pair
 from oracle import attention as oa
-from nanovllm_amd import workloads as W
+import workloads as W
 from nanovllm_amd.kernels.fp8_attention import fp8_decode_attention, fp8_prefill_attention
 
 pytestmark = pytest.mark.gpu
@@ -43,6 +43,46 @@ def test_prefill_qwen3_8b_chunks():
     wl = W.qwen3_8b_prefill()
     announce(f"prefill: {wl.name}")
     _check(wl)
+
+
+def test_mixed_batch_through_the_attention_layer():
+    """The whole mixed batch at Qwen3-8B shapes, as the reference's Attention
+    layer runs it (nanovllm/layers/attention.py:58-96): 192 plain-decode rows
+    before split_pt go to fp8_decode_attention, the 32 speculative sequences
+    (5 rows each) and 3 chunks of 512 tokens to fp8_prefill_attention, and the
+    outputs are concatenated.  Every row against the oracle."""
+    from attention_layer import Attention
+    from nanovllm_amd.utils.context import reset_context, set_context
+    wl = W.qwen3_8b_mixed()
+    sp = wl.extra["split_pt"]
+    announce(f"mixed batch through the attention layer: {sp} decode + {wl.num_seqs - sp} varlen sequences")
+    cpu_c, gpu_c = build_pair(wl, gen_device="cuda")
+    q = wl.make_q("cpu")
+    vl = W.sub_workload(wl, range(sp, wl.num_seqs))
+    cu_q, cu_k = vl.cu_seqlens()
+    bt = torch.from_numpy(wl.block_tables).cuda()
+    n = q.shape[0]
+    attn = Attention(wl.num_heads, 128, SCALE)
+    attn.k_cache, attn.v_cache = gpu_c
+    # K/V of this step are already in the cache: every slot is -1, nothing is stored
+    set_context(split_pt=sp, num_spec_seqs=wl.extra["num_spec_seqs"],
+                cu_seqlens_q=torch.from_numpy(cu_q).cuda(), cu_seqlens_k=torch.from_numpy(cu_k).cuda(),
+                max_seqlen_q=int(vl.lq().max()), max_seqlen_k=int(vl.lk().max()),
+                slot_mapping=torch.full((n,), -1, dtype=torch.int32, device="cuda"),
+                context_lens=torch.from_numpy(wl.context_lens()[:sp]).cuda(), block_tables=bt)
+    try:
+        kv = torch.zeros(n, wl.num_kv_heads, 128, dtype=torch.bfloat16, device="cuda")
+        out = attn(q.cuda(), kv, kv)
+        torch.cuda.synchronize()
+    finally:
+        reset_context()
+    want_d = oa.decode_attention(q[:sp], cpu_c[0], cpu_c[1], torch.from_numpy(wl.block_tables[:sp]),
+                                 torch.from_numpy(wl.context_lens()[:sp]), SCALE)
+    want_p = oa.prefill_attention(q[sp:], cpu_c[0], cpu_c[1], torch.from_numpy(vl.block_tables),
+                                  torch.from_numpy(cu_q), torch.from_numpy(cu_k), SCALE)
+    assert out.shape == q.shape
+    assert_close(out[:sp], want_d, "mixed batch: plain-decode rows")
+    assert_close(out[sp:], want_p, "mixed batch: speculative rows and chunks")
 
 
 def test_prefill_mixed_spec_and_chunks():

@@ -1,17 +1,27 @@
-"""Greedy decode on a random-init Qwen3: HIP attention vs the oracle.
+"""Free-running greedy decode on a random-init Qwen3: HIP attention vs the oracle.
 
-Two copies of the same random-init Qwen3 (Qwen3-0.6B attention shapes: 16
-query / 8 kv heads, head_dim 128; 2 layers, vocab 2048) differ only in their
-attention layer: the product path (FP8 store + HIP decode / prefill kernels)
-or the oracle on the CPU.  Both run the same schedule: 256-token chunked
-prefill of prompts of 37, 300, 513 and 129 tokens (so one step mixes decode
-rows with prefill chunks, and one chunk has a single token), plain decode
-steps, and one step where two sequences carry three speculative drafts.
-Every predicting row's logits must agree within tolerance, and the greedy
-token must be identical on every row whose oracle top-2 margin exceeds twice
-that row's observed logit difference (closer margins are numerical ties that
-the perturbation could reorder; both runs then continue with the oracle's
-token).
+Two copies of the same random-init Qwen3 at Qwen3-8B attention shapes (32
+query / 8 kv heads, head_dim 128; hidden 2048, vocab 2048) differ only in
+their attention layer: the product path (FP8 store + HIP decode / prefill
+kernels) or the oracle on the CPU.  Each copy runs free: it feeds back its
+OWN greedy token.  Both run the same schedule -- 256-token chunked prefill of
+prompts of 37, 300, 513 and 129 tokens (steps mix decode rows with prefill
+chunks; one chunk has a single token), plain decode steps, and two steps in
+which two sequences carry three speculative drafts (verification rows).
+
+The test fails on any divergence: every predicting row (including each
+speculative verification row) must have the same greedy token in both runs,
+and the generated token sequences must be identical after the last step.
+Rows whose oracle top-2 margin is within the row's observed logit
+deviation are reported (printed), not excused.
+
+Seeds: the two runs' logits differ by up to ~0.09 (two layers) or ~0.045
+(one layer) -- the fp16 P of the kernels and the bf16 output rounding flip
+single bf16 ulps of some attention outputs, which the second layer's FP8
+re-quantisation of K/V amplifies.  A random-init LM head has top-2 margins
+distributed down to 0, so some seeds contain a numerical tie that either
+implementation could break either way; the seeds below have none (minimum
+top-2 margins 0.057 and 0.049 over their 89 rows on MI355X).
 """
 import copy
 
@@ -21,57 +31,62 @@ import torch
 from gpu_util import announce
 from qwen3_harness import GreedyRunner, Qwen3TinyConfig, hip_model, make_sequences, oracle_model
 
-# Both models keep bf16 activations and both attention paths round their
-# output to bf16 (one ulp = 2**-8 relative); the HIP kernels also feed P to the
-# MFMA in bf16.  Single-ulp flips in attention outputs, carried through two
-# bf16 layers, move logits of magnitude ~10 by up to ~1% of their range, so
-# logits are compared at 2.5% of that range; greedy tokens must be identical.
+# Both models keep bf16 activations and round attention outputs to bf16; a
+# gross attention error moves logits by O(1), far outside this tolerance.
 LOGIT_TOL = dict(atol=0.25, rtol=2e-2)
+PROMPTS = [37, 300, 513, 129]
+STEPS = 20
+SPEC_STEPS = {7: {1, 3}, 13: {0, 2}}
+DRAFTS = [7, 1000, 42]
 
 
 @pytest.mark.gpu
-def test_greedy_tokens_identical_to_oracle():
-    announce("qwen3 greedy: 2 layers, prompts [37, 300, 513, 129], 20 steps, spec steps 7 and 13")
-    cfg = Qwen3TinyConfig()
+@pytest.mark.parametrize("layers,seed", [(2, 7), (1, 1)])
+def test_free_running_greedy_sequences_identical(layers, seed):
+    announce(f"qwen3 greedy (free-running): {layers} layer(s), seed {seed}, 32/8 heads, "
+             f"prompts {PROMPTS}, {STEPS} steps, speculative steps {sorted(SPEC_STEPS)}")
+    cfg = Qwen3TinyConfig(num_layers=layers, hidden_size=2048, num_heads=32, num_kv_heads=8)
     num_blocks = 48
-    hip = hip_model(cfg, num_blocks, seed=11)
-    ora = oracle_model(cfg, num_blocks, seed=11)
-    seqs_h = make_sequences([37, 300, 513, 129], 24, cfg.vocab_size, cfg.block_size, num_blocks, seed=5)
+    hip = hip_model(cfg, num_blocks, seed=seed)
+    ora = oracle_model(cfg, num_blocks, seed=seed)
+    seqs_h = make_sequences(PROMPTS, 24, cfg.vocab_size, cfg.block_size, num_blocks, seed=seed + 100)
     seqs_o = copy.deepcopy(seqs_h)
     run_h = GreedyRunner(hip, cfg.block_size, chunk=256)
     run_o = GreedyRunner(ora, cfg.block_size, chunk=256)
-    worst, min_margin, n_tokens, n_ties = 0.0, float("inf"), 0, 0
-    for step in range(20):
-        spec = {1, 3} if step == 7 else ({0, 2} if step == 13 else set())
+    worst, min_margin, n_rows, near_ties = 0.0, float("inf"), 0, []
+    for step in range(STEPS):
+        spec = SPEC_STEPS.get(step, set())
         for sq in (seqs_h, seqs_o):
             for i in spec:
-                sq[i].drafts = [7, 1000, 42]
+                sq[i].drafts = list(DRAFTS)
         out_h = run_h.step(seqs_h, spec)
         out_o = run_o.step(seqs_o, spec)
         assert sorted(out_h) == sorted(out_o)
-        for i in out_h:
+        for i in sorted(out_h):
             lh, lo = out_h[i].cpu(), out_o[i].cpu()
             assert lh.shape == lo.shape
-            worst = max(worst, float((lh - lo).abs().max()))
-            print(f"[qwen3-greedy] step {step} seq {i} rows {lh.shape[0]}: max |dlogit| "
-                  f"{float((lh - lo).abs().max()):.4f}, max |logit| {float(lo.abs().max()):.2f}", flush=True)
+            dev = (lh - lo).abs().max(dim=-1).values
+            worst = max(worst, float(dev.max()))
             assert torch.allclose(lh, lo, **LOGIT_TOL), \
-                f"step {step} seq {i}: logits differ by up to {float((lh - lo).abs().max())}"
+                f"step {step} seq {i}: logits differ by up to {float(dev.max())}"
             top2 = lo.topk(2, dim=-1).values
             margins = (top2[:, 0] - top2[:, 1]).tolist()
             th, to = lh.argmax(-1).tolist(), lo.argmax(-1).tolist()
-            row_dev = (lh - lo).abs().max(dim=-1).values.tolist()
-            for r, (a, b, mg, dv) in enumerate(zip(th, to, margins, row_dev)):
-                if mg > 2.0 * dv:   # the observed perturbation cannot reorder the top two
-                    assert a == b, f"step {step} seq {i} row {r}: greedy token {a} != oracle {b} (margin {mg:.3f})"
-                    n_tokens += 1
-                else:
-                    n_ties += 1   # a numerical tie: either token is a correct greedy choice
+            for r, (a, b, mg, dv) in enumerate(zip(th, to, margins, dev.tolist())):
+                n_rows += 1
                 min_margin = min(min_margin, mg)
-            # both runs continue with the oracle's token
-            seqs_h[i].tokens.append(to[0])
+                if mg <= dv:
+                    near_ties.append((step, i, r, mg, dv))
+                    print(f"[qwen3-greedy] near tie: step {step} seq {i} row {r}: top-2 margin {mg:.4f} "
+                          f"<= |dlogit| {dv:.4f}", flush=True)
+                assert a == b, (f"step {step} seq {i} row {r}: HIP greedy token {a} != oracle {b} "
+                                f"(oracle top-2 margin {mg:.4f}, row |dlogit| {dv:.4f})")
+            # free-running: each run continues with its own greedy token
+            seqs_h[i].tokens.append(th[0])
             seqs_o[i].tokens.append(to[0])
-    print(f"[qwen3-greedy] {n_tokens} predicted rows with identical greedy tokens, {n_ties} near-ties "
-          f"(top-2 margin <= 2 x the row's |dlogit|); max |dlogit| {worst:.4f}; min margin {min_margin:.4f}",
-          flush=True)
-    assert n_tokens >= 60 and n_ties <= n_tokens // 4
+    for i, (a, b) in enumerate(zip(seqs_h, seqs_o)):
+        assert a.tokens == b.tokens, f"sequence {i}: generated tokens differ"
+    print(f"[qwen3-greedy] {layers} layer(s), seed {seed}: {n_rows} predicting rows, identical greedy tokens "
+          f"and sequences; max |dlogit| {worst:.4f}; min top-2 margin {min_margin:.4f}; "
+          f"{len(near_ties)} rows with margin <= their |dlogit|", flush=True)
+    assert n_rows >= 80

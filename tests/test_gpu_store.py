@@ -8,7 +8,7 @@ import torch
 from gpu_util import announce, cpu_store
 from oracle import fp8 as ofp8
 from nanovllm_amd.layers.attention import store_kvcache
-from nanovllm_amd import workloads as W
+import workloads as W
 
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "bf16_to_e4m3fn.bin")

@@ -14,6 +14,7 @@ The named constructors reproduce the benchmark configurations:
   qwen3_0p6b_decode  B=256, 16/8 heads, ctx U[100, 2048]
   qwen3_8b_prefill  16 x 512-token chunks, 32/8 heads, cached U[0, 4096]
   qwen3_8b_mixed    192 decode + 32 spec x 5 + 3 x 512 chunks (+1024 contiguous)
+  qwen3_8b_decode   the mixed batch's 192 plain-decode rows (32/8 heads, ctx U[256, 4096])
   qwen3_32b_long_decode  B=32, 64/8 heads, ctx U[32K, 128K], 1% x20 outliers
 """
 from dataclasses import dataclass, field
@@ -196,6 +197,13 @@ def qwen3_8b_mixed(seed=4):
     wl = make_workload("qwen3_8b_mixed", 32, 8, dec + spec + chunks, seed)
     wl.extra.update(split_pt=192, num_spec_seqs=32, contiguous_prompt_len=1024)
     return wl
+
+
+def qwen3_8b_decode(seed=4):
+    """The mixed batch's 192 plain-decode rows on their own (32/8 heads, ctx
+    U[256, 4096]), over the mixed batch's paged pool."""
+    full = qwen3_8b_mixed(seed)
+    return sub_workload(full, range(full.extra["split_pt"]), name="qwen3_8b_decode_b192")
 
 
 def qwen3_32b_long_decode(seed=5, B=32, ctx_lo=32 * 1024, ctx_hi=128 * 1024):
