@@ -27,6 +27,7 @@
  *   - Workspace: decode and prefill need `*_workspace_bytes()` bytes of
  *     device memory for split-KV partial results (0 when no split happens).
  *     Its contents need no initialisation and are scratch after the call.
+ *     nvamd_fp8_decode_attention_noalloc uses a library-held array instead.
  */
 #ifndef NVAMD_FP8_ATTENTION_H_
 #define NVAMD_FP8_ATTENTION_H_
@@ -45,6 +46,7 @@ extern "C" {
 #define NVAMD_ERR_LAUNCH 4
 
 /* ABI version of this header (bumped on any signature change). */
+#define NVAMD_ABI_VERSION 3
 int32_t nvamd_abi_version(void);
 
 /* Description of the last error on the calling thread ("" if none). */
@@ -100,6 +102,31 @@ int32_t nvamd_fp8_decode_attention(void* out, const void* q,
                                    int32_t max_num_blocks, float softmax_scale,
                                    int32_t part_tokens, void* workspace, int64_t workspace_bytes,
                                    void* stream);
+
+/*
+ * Paged decode that allocates nothing and takes no workspace.  This entry
+ * point has no counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture that must not
+ * allocate, tight serving loops, harnesses that forbid hipMalloc).
+ *
+ * Same arguments, semantics and kernels as nvamd_fp8_decode_attention with
+ * part_tokens = 0 (the library's partitioning), except that the scratch those
+ * kernels use (the balanced kernel's stage prefix and cut-pair partials, or
+ * the split-KV partials) lives in a device array the library holds on every
+ * GPU it runs on, NVAMD_NOALLOC_SCRATCH_BYTES (32 MiB) per GPU until the
+ * process ends.  Shapes whose workspace (nvamd_decode_workspace_bytes with
+ * part_tokens = 0) exceeds it are rejected with NVAMD_ERR_WORKSPACE before
+ * anything is launched.  The scratch needs no initialisation and keeps the
+ * last call's contents; all calls on one GPU share it, so calls that
+ * overlap on one GPU (different streams, not ordered) race.
+ */
+#define NVAMD_NOALLOC_SCRATCH_BYTES (32ll << 20)
+int32_t nvamd_fp8_decode_attention_noalloc(void* out, const void* q,
+                                           const void* k_cache, const void* v_cache,
+                                           const int32_t* block_tables, const int32_t* context_lens,
+                                           int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                                           int32_t head_dim, int64_t num_blocks, int32_t block_size,
+                                           int32_t max_num_blocks, float softmax_scale, void* stream);
 
 /* Workspace needed by nvamd_fp8_prefill_attention.  kv_cap is the static
  * upper bound of keys per sequence: max_num_blocks*block_size for the paged

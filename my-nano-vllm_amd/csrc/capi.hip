@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -10,6 +11,13 @@
 
 #include "kernels.h"
 #include "nvamd_fp8_attention.h"
+
+// Scratch of nvamd_fp8_decode_attention_noalloc: device memory the library
+// holds for the whole process on every GPU it runs on (each GPU has its own
+// copy of the array at its own address).  Host code never uses the array's
+// name as an address (it is a host-side stand-in): the device address comes
+// from hipGetSymbolAddress, once per device (noalloc_scratch below).
+static __device__ __align__(256) uint8_t scratch[NVAMD_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -34,6 +42,29 @@ int32_t ok() {
 int32_t launch_status(hipError_t e, const char* what) {
   if (e != hipSuccess) return fail(NVAMD_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
   return ok();
+}
+
+// Device address of `scratch` on the current device, looked up on the first
+// call on that device (with it current) and kept per device.
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+
+int32_t noalloc_scratch(const char* fn, void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(NVAMD_ERR_LAUNCH, "%s: hipGetDevice: %s", fn, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(NVAMD_ERR_UNSUPPORTED, "%s: device ordinal %d beyond %d", fn, dev, kMaxDevices);
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(NVAMD_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch) on device %d: %s", fn, dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev].store(p, std::memory_order_release);  // the same address if two threads race here
+  }
+  *out = p;
+  return NVAMD_OK;
 }
 
 int device_cu_count() {
@@ -155,7 +186,7 @@ int64_t schedule_bytes(int32_t num_seqs, int g, int32_t max_seqlen_q) {
 
 extern "C" {
 
-int32_t nvamd_abi_version(void) { return 2; }
+int32_t nvamd_abi_version(void) { return NVAMD_ABI_VERSION; }
 
 const char* nvamd_last_error(void) { return g_last_error.c_str(); }
 
@@ -192,13 +223,17 @@ int64_t nvamd_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t n
   return partial_bytes(batch, num_heads, ceil_div(kv_cap, part));
 }
 
-int32_t nvamd_fp8_decode_attention(void* out, const void* q, const void* k_cache, const void* v_cache,
-                                   const int32_t* block_tables, const int32_t* context_lens,
-                                   int32_t batch, int32_t num_heads, int32_t num_kv_heads,
-                                   int32_t head_dim, int64_t num_blocks, int32_t block_size,
-                                   int32_t max_num_blocks, float softmax_scale, int32_t part_tokens,
-                                   void* workspace, int64_t workspace_bytes, void* stream) {
-  static const char* fn = "fp8_decode_attention";
+}  // extern "C"
+
+namespace {
+
+// nvamd_fp8_decode_attention; with lib_scratch, the workspace is the
+// library's scratch array (workspace / workspace_bytes are ignored).
+int32_t decode_attention(const char* fn, void* out, const void* q, const void* k_cache, const void* v_cache,
+                         const int32_t* block_tables, const int32_t* context_lens, int32_t batch,
+                         int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int64_t num_blocks,
+                         int32_t block_size, int32_t max_num_blocks, float softmax_scale, int32_t part_tokens,
+                         void* workspace, int64_t workspace_bytes, void* stream, bool lib_scratch) {
   if (int32_t e = check_heads(fn, num_heads, num_kv_heads, head_dim)) return e;
   if (!(softmax_scale > 0.f) || !std::isfinite(softmax_scale))
     return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: softmax_scale must be positive and finite", fn);
@@ -219,6 +254,16 @@ int32_t nvamd_fp8_decode_attention(void* out, const void* q, const void* k_cache
     return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: block_tables has no columns", fn);
   if (!out || !q || !k_cache || !v_cache || !block_tables || !context_lens)
     return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+
+  if (lib_scratch) {
+    const int64_t need = nvamd_decode_workspace_bytes(batch, num_heads, num_kv_heads, max_num_blocks, block_size,
+                                                      part_tokens);
+    if (need > NVAMD_NOALLOC_SCRATCH_BYTES)
+      return fail(NVAMD_ERR_WORKSPACE, "%s: these shapes need %lld bytes of scratch, more than the %lld the library "
+                  "holds", fn, (long long)need, (long long)NVAMD_NOALLOC_SCRATCH_BYTES);
+    if (int32_t e = noalloc_scratch(fn, &workspace)) return e;
+    workspace_bytes = NVAMD_NOALLOC_SCRATCH_BYTES;
+  }
 
   nvamd::MqParams p{};
   p.q = static_cast<const uint16_t*>(q);
@@ -264,6 +309,31 @@ int32_t nvamd_fp8_decode_attention(void* out, const void* q, const void* k_cache
                 (long long)need, (long long)workspace_bytes);
   set_partials(p, need > 0 ? workspace : nullptr);
   return launch_status(nvamd::launch_paged_mq(p, ncb, (hipStream_t)stream), fn);
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t nvamd_fp8_decode_attention(void* out, const void* q, const void* k_cache, const void* v_cache,
+                                   const int32_t* block_tables, const int32_t* context_lens,
+                                   int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                                   int32_t head_dim, int64_t num_blocks, int32_t block_size,
+                                   int32_t max_num_blocks, float softmax_scale, int32_t part_tokens,
+                                   void* workspace, int64_t workspace_bytes, void* stream) {
+  return decode_attention("fp8_decode_attention", out, q, k_cache, v_cache, block_tables, context_lens, batch,
+                          num_heads, num_kv_heads, head_dim, num_blocks, block_size, max_num_blocks, softmax_scale,
+                          part_tokens, workspace, workspace_bytes, stream, false);
+}
+
+int32_t nvamd_fp8_decode_attention_noalloc(void* out, const void* q, const void* k_cache, const void* v_cache,
+                                           const int32_t* block_tables, const int32_t* context_lens,
+                                           int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                                           int32_t head_dim, int64_t num_blocks, int32_t block_size,
+                                           int32_t max_num_blocks, float softmax_scale, void* stream) {
+  return decode_attention("fp8_decode_attention_noalloc", out, q, k_cache, v_cache, block_tables, context_lens,
+                          batch, num_heads, num_kv_heads, head_dim, num_blocks, block_size, max_num_blocks,
+                          softmax_scale, 0, nullptr, 0, stream, true);
 }
 
 int64_t nvamd_prefill_workspace_bytes(int64_t num_tokens, int32_t num_seqs, int32_t num_heads,
