@@ -64,6 +64,9 @@ constexpr int kVElems = kHeadDim * kVPitch;   // 9216
 constexpr int kBufElems = kKElems + kVElems;  // 17920 16-bit = 35840 B per K + V pair
 constexpr int kBtWindow = 64;                 // block-table entries held in one register
 constexpr int kLead = 4;                      // MFMA operands are read from LDS this many MFMAs ahead
+// A tile's row sum of fp16 weights above this moves the reference maximum
+// (every weight is then at most this, far below the fp16 maximum 65504).
+constexpr float kRowSumLimit = 16384.0f;
 
 // One staging thread's share of a K or V tile (see the staging geometry in
 // the kernel): K rows s/8 (r[0], r[1]) and s/8 + 32 (r[2], r[3]), bytes
@@ -206,8 +209,13 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
   const uint32_t v_off = (uint32_t)(4 * v_tg * rs + v_byte);
   const uint32_t urs = (uint32_t)rs;
 
-  // Block-table window: lane l holds entry win_base + l (paged layout).
-  int bt_lane = 0, win_base = 0;
+  // Block-table window (paged layout): lane l holds the byte offset in the
+  // cache of kv head g's slice of block entry win_base + l, as two dwords
+  // (-1 when the entry is not a usable block), computed once per window so
+  // that a tile's descriptor takes a few scalar instructions.
+  uint32_t blk_lo = 0, blk_hi = 0;
+  int win_base = 0;
+  const uint32_t tile_bytes = (uint32_t)(kBN * rs);  // one tile's rows of a block
 
   // Buffer descriptor of tile t of this wave's role (K or V).  Tiles past
   // the item (or with an invalid block) get zero-length descriptors: their
@@ -215,22 +223,25 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
   auto tile_rsrc = [&](int t) {
     const int kv0 = t * kBN;
     int nvalid = (t < n_tiles) ? min(kBN, Lk - kv0) : 0;
-    int64_t row0 = 0;
+    int64_t base = 0;
     if constexpr (PAGED) {
       // block of tile t by a multiply with the reciprocal of the tiles per
       // block (exact for t < 2^31 / tpb; a division would be dozens of
       // instructions and a branch)
       const int bi = (int)__umulhi((uint32_t)t << 1, p.tpb_magic);
-      const int blk = __builtin_amdgcn_readlane(bt_lane, min(max(bi - win_base, 0), kBtWindow - 1));
-      row0 = (int64_t)blk * p.block_size + (t - bi * p.tpb) * kBN;
-      if (blk < 0 || row0 + kBN > p.kv_rows) nvalid = 0;
+      const int l = min(max(bi - win_base, 0), kBtWindow - 1);
+      const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)blk_lo, l);
+      const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)blk_hi, l);
+      const int64_t boff = (int64_t)(((uint64_t)hi << 32) | lo);
+      if (boff < 0) nvalid = 0;
+      base = boff + (int64_t)((uint32_t)(t - bi * p.tpb) * tile_bytes);
     } else {
-      row0 = (int64_t)k_start + kv0;
+      const int64_t row0 = (int64_t)k_start + kv0;
       if (row0 < 0 || row0 + max(nvalid, 0) > p.kv_rows) nvalid = 0;
+      base = (row0 * p.Hkv + g) * kHeadDim;
     }
     nvalid = max(nvalid, 0);
-    if (nvalid == 0) row0 = 0;
-    const int64_t base = (row0 * p.Hkv + g) * kHeadDim;
+    if (nvalid == 0) base = 0;
     const uint32_t nbytes = (uint32_t)(nvalid * rs);
     return make_rsrc((k_role ? p.k : p.v) + base, nbytes);
   };
@@ -338,10 +349,10 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
   };
   // Row maximum of tile s in pieces: elements 8q..8q+7, then the running
   // maximum is moved from the maximum of the pieces (raw scores; the scale
-  // is positive): the lanes whose maximum exceeds the reference by more than
-  // kLazyRescaleLog2 move it (lazy rescale).  The update scales the row sum
-  // and returns whether any lane moved; alpha is the factor for the
-  // accumulators.
+  // is positive) on the lanes where it exceeds the reference.  Used on the
+  // first tile of a block-table window and when a tile's weights grow past
+  // kRowSumLimit.  The update scales the row sum and returns whether any
+  // lane moved; alpha is the factor for the accumulators.
   auto max8 = [&](const f32x16 (&s)[2], int q) {
     const int rb = q >> 1, o = 8 * (q & 1);
     float m = fmaxf(s[rb][o], s[rb][o + 1]);
@@ -356,7 +367,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
       const uint32_t s0 = sw[0], s1 = sw[1];
       mx = fmaxf(__builtin_bit_cast(float, s0), __builtin_bit_cast(float, s1)) * p.scale_log2;
     }
-    const bool grow = mx > m_run + kLazyRescaleLog2;
+    const bool grow = mx > m_run;
     alpha = grow ? fast_exp2(m_run - mx) : 1.f;
     m_run = grow ? mx : m_run;
     m_use = (m_run == -INFINITY) ? 0.f : m_run;
@@ -413,45 +424,59 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       if (i < 11) __builtin_amdgcn_sched_group_barrier(0x402, 6, 0);
     }
-    l_run += ps_pend;
 #pragma unroll
     for (int i = 4; i < 16; ++i) pin(pw[i]);
 #pragma unroll
     for (int i = 0; i < kLead; ++i) pin(vpre[i]);
-    pin(l_run);
+    pin(ps_pend);
   };
 
   // Part B places its work by hand, one segment per MFMA (sched_barrier
-  // fences): the loads, the row maximum of S_{t+1} in four pieces, its
-  // exchange and the running-maximum update, the staging in four quarters,
-  // and S_{t+1}'s words 0..3, one per segment.
+  // fences): the loads, the staging in four quarters, and S_{t+1}'s words
+  // 0..3, one per segment.  S_{t+1} is exponentiated against the current
+  // reference maximum without taking its row maximum first; the step checks
+  // the resulting row sum instead (see full_step).
   auto part_b = [&](const uint16_t* vb, u32x4 (&vpre)[kLead], const uint32_t (&pw)[16], const f32x16 (&s_next)[2],
-                    uint32_t (&pw_next)[16], float& alpha, bool& any_grow, auto&& loads, auto&& stage_quarter) {
+                    uint32_t (&pw_next)[16], auto&& loads, auto&& stage_quarter) {
     f16x8 pop[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) pop[ks] = as_f16x8(pw[4 * ks], pw[4 * ks + 1], pw[4 * ks + 2], pw[4 * ks + 3]);
-    float mq[4];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const u32x4 cur = vpre[i % kLead];
       if (i + kLead < 16) vpre[i % kLead] = *reinterpret_cast<const u32x4*>(vaddr(vb, i + kLead));
       acc[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(cur), pop[i >> 2], acc[i & 3], 0, 0, 0);
       if (i == 0) loads();
-      if (i >= 2 && i < 6) mq[i - 2] = max8(s_next, i - 2);
-      if (i == 6) any_grow = update_max_from(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3])), alpha);
-      if (i == 7) stage_quarter(std::integral_constant<int, 0>{});
-      if (i == 8) stage_quarter(std::integral_constant<int, 1>{});
-      if (i == 9) stage_quarter(std::integral_constant<int, 2>{});
-      if (i == 10) stage_quarter(std::integral_constant<int, 3>{});
-      if (i == 11) ps_pend = 0.f;
-      if (i >= 11 && i < 15) exp_pair(s_next, i - 11, pw_next, ps_pend);
+      if (i == 3) stage_quarter(std::integral_constant<int, 0>{});
+      if (i == 5) stage_quarter(std::integral_constant<int, 1>{});
+      if (i == 7) stage_quarter(std::integral_constant<int, 2>{});
+      if (i == 9) stage_quarter(std::integral_constant<int, 3>{});
+      if (i == 10) ps_pend = 0.f;
+      if (i >= 10 && i < 14) exp_pair(s_next, i - 10, pw_next, ps_pend);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) pin(pw_next[j]);
     pin(ps_pend);
-    pin(l_run);
-    pin(m_use);
+  };
+
+  // The weights of a tile are exp2(s * scale - m_use) with m_use the running
+  // reference maximum, so they stay bounded as long as no score exceeds it
+  // by much.  A lane's row sum of the tile's fp16 weights (ps_pend) above
+  // kRowSumLimit (or infinite: an fp16 overflow) means some score did: the
+  // reference maximum then moves to the row maximum of the tile, the
+  // accumulators and row sum are rescaled, and the tile's 16 words are
+  // computed again.  Rare (at most once per growth of the maximum by more
+  // than log2(kRowSumLimit / 32)); every weight used is <= kRowSumLimit.
+  auto check_tile = [&](const f32x16 (&s)[2], uint32_t (&pw)[16]) {
+    if (wave_any(!(ps_pend <= kRowSumLimit))) {
+      float alpha;
+      if (update_max(s, alpha)) rescale_acc(alpha);
+      ps_pend = 0.f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) exp_pair(s, j, pw, ps_pend);
+    }
+    l_run += ps_pend;
   };
 
   // ---- tile loop, one block-table window at a time -----------------------------
@@ -475,7 +500,11 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
     if constexpr (PAGED) {
       win_base = (t0 * kBN) / p.block_size;
       const int bi = min(win_base + lane, (int)p.bt_stride - 1);
-      bt_lane = p.block_tables[(int64_t)seq * p.bt_stride + bi];
+      const int blk = p.block_tables[(int64_t)seq * p.bt_stride + bi];
+      const int64_t row = (int64_t)blk * p.block_size;
+      const int64_t off = (blk >= 0 && row + p.block_size <= p.kv_rows) ? (row * p.Hkv + g) * kHeadDim : -1;
+      blk_lo = (uint32_t)off;
+      blk_hi = (uint32_t)((uint64_t)off >> 32);
     }
     auto in_win = [&](int t) { return t < t1 ? t : n_tiles; };
     TileRegs ra, rb;
@@ -524,12 +553,10 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
                          uint16_t* stage_vb, TileRegs& load_regs) {
       u32x4 vpre[kLead];
       part_a(kb_next, vb, s_cur, s_next, pw, vpre);
+      check_tile(s_cur, pw);
       mask_tile(t + 1, t1, s_next);
-      float alpha = 1.f;
-      bool any_grow = false;
-      part_b(vb, vpre, pw, s_next, pw_next, alpha, any_grow, [&] { load(role, in_win(t + 3), in_win(t + 2), load_regs); },
+      part_b(vb, vpre, pw, s_next, pw_next, [&] { load(role, in_win(t + 3), in_win(t + 2), load_regs); },
              [&](auto qc) { stage_q(role, stage_regs, stage_kb, stage_vb, qc); });
-      if (any_grow) rescale_acc(alpha);
       wait_lds();
       __syncthreads();
     };
