@@ -20,7 +20,8 @@
  *   - bf16 tensors are passed as raw 16-bit storage; FP8 tensors hold OCP
  *     E4M3FN bytes (torch.float8_e4m3fn).  Integer metadata is int32.
  *   - head_dim must be 128 for the attention kernels; block_size must be a
- *     positive multiple of 64.
+ *     positive multiple of 16 (the reference's kvcache_block_size rule,
+ *     nanovllm/config.py:30).
  *   - Return value: NVAMD_OK (0) or an NVAMD_ERR_* code; nvamd_last_error()
  *     then describes the failure (thread-local, valid until the next call
  *     on the same thread).

@@ -239,8 +239,8 @@ int32_t decode_attention(const char* fn, void* out, const void* q, const void* k
     return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: softmax_scale must be positive and finite", fn);
   if (batch < 0 || num_blocks < 0 || max_num_blocks < 0)
     return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: negative size", fn);
-  if (block_size <= 0 || block_size % 64 != 0)
-    return fail(NVAMD_ERR_UNSUPPORTED, "%s: block_size must be a positive multiple of 64 (got %d)", fn, block_size);
+  if (block_size <= 0 || block_size % 16 != 0)
+    return fail(NVAMD_ERR_UNSUPPORTED, "%s: block_size must be a positive multiple of 16 (got %d)", fn, block_size);
   if (part_tokens < 0 || part_tokens % kPartAlign != 0)
     return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: part_tokens must be 0 or a multiple of %d", fn, kPartAlign);
   if (part_tokens > max_part_tokens(block_size))
@@ -366,10 +366,15 @@ int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, con
   if (num_tokens < 0 || num_seqs < 0 || num_kv_rows < 0 || max_seqlen_q < 0)
     return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: negative size", fn);
   const bool paged = block_tables != nullptr;
-  if (paged && (block_size <= 0 || block_size % 64 != 0))
-    return fail(NVAMD_ERR_UNSUPPORTED, "%s: block_size must be a positive multiple of 64 (got %d)", fn, block_size);
+  if (paged && (block_size <= 0 || block_size % 16 != 0))
+    return fail(NVAMD_ERR_UNSUPPORTED, "%s: block_size must be a positive multiple of 16 (got %d)", fn, block_size);
   if (paged && max_num_blocks <= 0)
     return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: block_tables has no columns", fn);
+  // the prefill kernel finds a key's block by a reciprocal multiply, exact
+  // below 2^35 / block_size keys per sequence
+  if (paged && (int64_t)max_num_blocks * block_size >= (1ll << 35) / block_size)
+    return fail(NVAMD_ERR_UNSUPPORTED, "%s: %d blocks of %d tokens per sequence exceed the addressable keys", fn,
+                max_num_blocks, block_size);
   if (part_tokens < 0 || part_tokens % kPartAlign != 0)
     return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: part_tokens must be 0 or a multiple of %d", fn, kPartAlign);
   if (paged && part_tokens > max_part_tokens(block_size))
@@ -463,8 +468,7 @@ int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, con
   pp.n_hgroups = G / pp.GW;
   pp.n_mblocks = (int)ceil_div(max_seqlen_q, pp.BM);
   pp.block_size = paged ? block_size : 64;
-  pp.tpb = pp.block_size / 64;
-  pp.tpb_magic = (uint32_t)(((1u << 31) - 1u) / (uint32_t)pp.tpb + 1u);
+  pp.blk_magic = (uint32_t)(((1u << 31) - 1u) / (uint32_t)(pp.block_size / 16) + 1u);
   pp.mq_max_q = mq_max_q;
   pp.scale_log2 = softmax_scale * 1.4426950408889634f;
   void* schedule = static_cast<char*>(workspace) + align_up(partials);

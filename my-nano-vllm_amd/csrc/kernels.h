@@ -65,9 +65,8 @@ struct PrefillParams {
   int BM;         // query tokens per workgroup (32 * kPrefillWaves / GW)
   int n_hgroups;  // G / GW
   int n_mblocks;  // ceil(max_seqlen_q / BM)
-  int block_size;
-  int tpb;            // 64-token tiles per block (block_size / 64)
-  uint32_t tpb_magic;  // ceil(2^31 / tpb): block of tile t = umulhi(2t, tpb_magic)
+  int block_size;      // a multiple of 16 (paged layout)
+  uint32_t blk_magic;  // ceil(2^31 / (block_size / 16)): block of key kv = umulhi(2 * (kv >> 4), blk_magic)
   int mq_max_q;   // sequences with Lq <= mq_max_q are left to the short-query kernel
   float scale_log2;
 };

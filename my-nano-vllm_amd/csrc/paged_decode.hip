@@ -389,31 +389,42 @@ __device__ __forceinline__ void mq_attn(const MqParams& p, const int part, const
   // Instruction j (= 2*wave + i) covers stage rows [j*kRowsPerLoad, +kRowsPerLoad);
   // lane l fetches row j*kRowsPerLoad + l/kLanesPerRow, granule
   // (l % kLanesPerRow) ^ (row & 7), and lands at LDS offset j*1024 + 16*l.
+  // The wave's rows [wr0, wr0 + kWaveRows) get a descriptor of their own
+  // (offsets relative to row wr0): they start at a multiple of kWaveRows
+  // (8 or 16) from the partition start, so they lie in one KV block
+  // whenever block_size % 16 == 0, even when a stage spans several blocks.
+  constexpr int kWaveRows = 2 * S::kRowsPerLoad;
+  const int wr0 = wave * kWaveRows;
   uint32_t fetch_off[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int row = (2 * wave + i) * S::kRowsPerLoad + lane / S::kLanesPerRow;
     const int gran = (lane % S::kLanesPerRow) ^ (row & 7);
-    fetch_off[i] = (uint32_t)row * (uint32_t)rs + 16u * (uint32_t)gran;
+    fetch_off[i] = (uint32_t)(row - wr0) * (uint32_t)rs + 16u * (uint32_t)gran;
   }
 
-  // Stage cursor (paged layout): a stage never straddles a KV block
-  // (block_size % 64 == 0).  The partition's block-table entries are loaded
-  // once, lane l holding entry first_bi + l (a partition spans at most
-  // kMaxPartBlocks blocks, enforced by the host), and read in the loop with
-  // v_readlane, so the loop issues no memory reads besides the stages.
-  // Table indices are clamped into the row: entries past the partition are
-  // never dereferenced (their stages get zero-length descriptors).
+  // Cursor of the wave's rows (paged layout): block index w_bi (relative to
+  // the partition's first block) and row offset w_off in it.  The
+  // partition's block-table entries are loaded once, lane l holding entry
+  // first_bi + l (a partition spans at most kMaxPartBlocks blocks, enforced
+  // by the host), and read in the loop with v_readlane, so the loop issues
+  // no memory reads besides the stages.  Table indices are clamped into the
+  // row: entries past the partition are never dereferenced (their stages
+  // get zero-length descriptors).
   const bool paged = p.block_tables != nullptr;
-  int ld_tok = kv_begin;
-  int ld_bi = 0, ld_off = 0, bt_lane = 0;
+  int ld_tok = kv_begin + wr0;  // the wave's first row of the next stage
+  int w_bi = 0, w_off = 0, bt_lane = 0;
   if (paged) {
     const int first_bi = kv_begin / p.block_size;
-    ld_off = kv_begin - first_bi * p.block_size;
+    w_off = kv_begin + wr0 - first_bi * p.block_size;
+    while (w_off >= p.block_size) {
+      w_off -= p.block_size;
+      ++w_bi;
+    }
     const int bi = min(first_bi + lane, (int)p.bt_stride - 1);
     bt_lane = p.block_tables[(int64_t)seq * p.bt_stride + bi];
   }
-  auto cur_block = [&]() -> int { return __builtin_amdgcn_readlane(bt_lane, min(ld_bi, 63)); };
+  auto cur_block = [&]() -> int { return __builtin_amdgcn_readlane(bt_lane, min(w_bi, 63)); };
 
   // Issues this wave's share of the cursor's stage into ring slot `slot`
   // and advances the cursor.  Rows past the partition (or an invalid block)
@@ -421,12 +432,12 @@ __device__ __forceinline__ void mq_attn(const MqParams& p, const int part, const
   // iteration has the same loads in flight, but they read nothing and write
   // zeros.
   auto issue_stage = [&](int slot) {
-    int nvalid = max(0, min(S::kTS, kv_end - ld_tok));
+    int nvalid = max(0, min(kWaveRows, kv_end - ld_tok));
     int64_t row;
     if (paged) {
       const int blk = cur_block();
-      row = (int64_t)blk * p.block_size + ld_off;
-      if (blk < 0 || row + S::kTS > p.kv_rows) nvalid = 0;
+      row = (int64_t)blk * p.block_size + w_off;
+      if (blk < 0 || row + kWaveRows > p.kv_rows) nvalid = 0;
     } else {
       row = (int64_t)sg.kv_row0 + ld_tok;
       if (row < 0 || row + nvalid > p.kv_rows) nvalid = 0;
@@ -442,10 +453,10 @@ __device__ __forceinline__ void mq_attn(const MqParams& p, const int part, const
     dma_load16(rv, fetch_off[0], dst + (uint32_t)S::kHalf);
     dma_load16(rv, fetch_off[1], dst + (uint32_t)S::kHalf + 1024u);
     ld_tok += S::kTS;
-    ld_off += S::kTS;
-    if (ld_off >= p.block_size) {
-      ld_off -= p.block_size;
-      ++ld_bi;
+    w_off += S::kTS;
+    while (w_off >= p.block_size) {  // at most kTS / 16 blocks per stage
+      w_off -= p.block_size;
+      ++w_bi;
     }
   };
 

@@ -115,7 +115,7 @@ __device__ __forceinline__ void pin(T& v) { asm volatile("" : "+v"(v)); }
 // ---------------------------------------------------------------------------
 // Main kernel
 // ---------------------------------------------------------------------------
-template <bool PAGED>
+template <bool PAGED, bool SMALL_BLOCKS>
 __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(PrefillParams p,
                                                                               const PrefillItem* __restrict__ items,
                                                                               MqParams mq, int n_main) {
@@ -204,39 +204,45 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
   // Lanes 4..7 of each K row store (and so load) their high 8 fp8 first,
   // so each store instruction's 8-lane groups cover all banks of the row.
   const int k_first = (stid & 4) ? 8 : 0;
-  const uint32_t k_off0 = (uint32_t)(k_row * rs + k_byte + k_first);
-  const uint32_t k_off1 = (uint32_t)((k_row + 32) * rs + k_byte + k_first);
-  const uint32_t v_off = (uint32_t)(4 * v_tg * rs + v_byte);
   const uint32_t urs = (uint32_t)rs;
+  // With SMALL_BLOCKS (block_size % 64 != 0, a tile may span several
+  // blocks) a wave's load instructions, which cover 8 consecutive tile rows
+  // (K: rows kg0 + [0, 8) and kg0 + 32 + [0, 8)) or 16 (V: rows vg0 +
+  // [0, 16)) that lie in one block whenever block_size % 16 == 0, get a
+  // descriptor per row group, and the lanes' offsets are relative to its
+  // first row; otherwise one descriptor covers the tile.
+  const int kg0 = SMALL_BLOCKS ? 8 * (stid >> 6) : 0, vg0 = SMALL_BLOCKS ? 16 * (stid >> 6) : 0;
+  const uint32_t k_rel = (uint32_t)((k_row - kg0) * rs + k_byte + k_first);
+  const uint32_t k_rel_hi = SMALL_BLOCKS ? k_rel : (uint32_t)((k_row + 32) * rs + k_byte + k_first);
+  const uint32_t v_rel = (uint32_t)(4 * (v_tg - vg0 / 4) * rs + v_byte);
 
   // Block-table window (paged layout): lane l holds the byte offset in the
   // cache of kv head g's slice of block entry win_base + l, as two dwords
   // (-1 when the entry is not a usable block), computed once per window so
-  // that a tile's descriptor takes a few scalar instructions.
+  // that a descriptor takes a few scalar instructions.
   uint32_t blk_lo = 0, blk_hi = 0;
   int win_base = 0;
-  const uint32_t tile_bytes = (uint32_t)(kBN * rs);  // one tile's rows of a block
 
-  // Buffer descriptor of tile t of this wave's role (K or V).  Tiles past
-  // the item (or with an invalid block) get zero-length descriptors: their
-  // loads read nothing.
-  auto tile_rsrc = [&](int t) {
-    const int kv0 = t * kBN;
-    int nvalid = (t < n_tiles) ? min(kBN, Lk - kv0) : 0;
+  // Buffer descriptor of rows [r0, r0 + nrows) of tile t.  Rows past the
+  // item's keys (or in an invalid block, or of tiles past the item) are
+  // outside the descriptor's range: their loads read zeros.
+  auto group_rsrc = [&](int t, int r0, int nrows) {
+    const int kv = t * kBN + r0;
+    int nvalid = (t < n_tiles) ? min(nrows, Lk - kv) : 0;
     int64_t base = 0;
     if constexpr (PAGED) {
-      // block of tile t by a multiply with the reciprocal of the tiles per
-      // block (exact for t < 2^31 / tpb; a division would be dozens of
-      // instructions and a branch)
-      const int bi = (int)__umulhi((uint32_t)t << 1, p.tpb_magic);
+      // block of key kv by a multiply with the reciprocal of the block size
+      // in 16-token units (exact for kv < 2^35 / block_size, which the host
+      // checks; a division would be dozens of instructions and a branch)
+      const int bi = (int)__umulhi((uint32_t)(kv >> 4) << 1, p.blk_magic);
       const int l = min(max(bi - win_base, 0), kBtWindow - 1);
       const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)blk_lo, l);
       const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)blk_hi, l);
       const int64_t boff = (int64_t)(((uint64_t)hi << 32) | lo);
       if (boff < 0) nvalid = 0;
-      base = boff + (int64_t)((uint32_t)(t - bi * p.tpb) * tile_bytes);
+      base = boff + (int64_t)((uint32_t)(kv - bi * p.block_size) * urs);
     } else {
-      const int64_t row0 = (int64_t)k_start + kv0;
+      const int64_t row0 = (int64_t)k_start + kv;
       if (row0 < 0 || row0 + max(nvalid, 0) > p.kv_rows) nvalid = 0;
       base = (row0 * p.Hkv + g) * kHeadDim;
     }
@@ -250,15 +256,17 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
   // for K) so that no branch splits the code the loads are scheduled into.
   auto load = [&](auto role, int t, int tv, TileRegs& r) {
     constexpr bool kRole = decltype(role)::value;
-    const __amdgpu_buffer_rsrc_t rs_ = tile_rsrc(kRole ? t : tv);
     if constexpr (kRole) {
-      r.r[0] = buf_load8(rs_, k_off0);
-      r.r[1] = buf_load8(rs_, k_off0 ^ 8u);
-      r.r[2] = buf_load8(rs_, k_off1);
-      r.r[3] = buf_load8(rs_, k_off1 ^ 8u);
+      const __amdgpu_buffer_rsrc_t lo = SMALL_BLOCKS ? group_rsrc(t, kg0, 8) : group_rsrc(t, 0, kBN);
+      const __amdgpu_buffer_rsrc_t hi = SMALL_BLOCKS ? group_rsrc(t, kg0 + 32, 8) : lo;
+      r.r[0] = buf_load8(lo, k_rel);
+      r.r[1] = buf_load8(lo, k_rel ^ 8u);
+      r.r[2] = buf_load8(hi, k_rel_hi);
+      r.r[3] = buf_load8(hi, k_rel_hi ^ 8u);
     } else {
+      const __amdgpu_buffer_rsrc_t rv = SMALL_BLOCKS ? group_rsrc(tv, vg0, 16) : group_rsrc(tv, 0, kBN);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) r.r[e] = buf_load8(rs_, v_off + (uint32_t)e * urs);
+      for (int e = 0; e < 4; ++e) r.r[e] = buf_load8(rv, v_rel + (uint32_t)e * urs);
     }
   };
 
@@ -627,10 +635,12 @@ hipError_t launch_varlen_prefill(const PrefillParams& p, const void* schedule, c
   if (n_blocks + n_merge > 0x7fffffff || schedule == nullptr) return hipErrorInvalidValue;
   const dim3 grid((unsigned)(n_blocks + n_merge)), block(64 * kPrefillWaves);
   const PrefillItem* items = static_cast<const PrefillItem*>(schedule);
-  if (p.block_tables != nullptr)
-    hipLaunchKernelGGL(varlen_prefill_kernel<true>, grid, block, 0, stream, p, items, mq, (int)n_blocks);
+  if (p.block_tables == nullptr)
+    hipLaunchKernelGGL((varlen_prefill_kernel<false, false>), grid, block, 0, stream, p, items, mq, (int)n_blocks);
+  else if (p.block_size % kBN == 0)
+    hipLaunchKernelGGL((varlen_prefill_kernel<true, false>), grid, block, 0, stream, p, items, mq, (int)n_blocks);
   else
-    hipLaunchKernelGGL(varlen_prefill_kernel<false>, grid, block, 0, stream, p, items, mq, (int)n_blocks);
+    hipLaunchKernelGGL((varlen_prefill_kernel<true, true>), grid, block, 0, stream, p, items, mq, (int)n_blocks);
   return hipGetLastError();
 }
 

@@ -40,8 +40,14 @@ def test_rejects_bad_gqa_and_block_size_without_gpu():
     lib = _native.load()
     assert lib.nvamd_fp8_decode_attention(None, None, None, None, None, None, 4, 6, 4, 128, 16, 256, 4,
                                           0.1, 0, None, 0, None) == 1
-    assert lib.nvamd_fp8_decode_attention(None, None, None, None, None, None, 4, 8, 2, 128, 16, 48, 4,
+    # block sizes must be multiples of 16 (nanovllm/config.py:30): 40 is rejected as unsupported;
+    # 48 passes that check and fails later on the null pointers
+    assert lib.nvamd_fp8_decode_attention(None, None, None, None, None, None, 4, 8, 2, 128, 16, 40, 4,
                                           0.1, 0, None, 0, None) == 2
+    assert b"multiple of 16" in lib.nvamd_last_error()
+    assert lib.nvamd_fp8_decode_attention(None, None, None, None, None, None, 4, 8, 2, 128, 16, 48, 4,
+                                          0.1, 0, None, 0, None) == 1
+    assert b"null pointer" in lib.nvamd_last_error()
     assert lib.nvamd_fp8_prefill_attention(None, None, None, None, None, None, None, 4, 1, 8, 2, 128, 100,
                                            256, 2, 4, 4, 0.1, 100, None, 0, None) == 1  # part_tokens % 256
     assert b"part_tokens" in lib.nvamd_last_error()

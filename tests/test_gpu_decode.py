@@ -209,3 +209,23 @@ def test_decode_long_context_outliers_full_size():
     want = oa.decode_attention(q[pick].cpu(), kc_s, vc_s, torch.from_numpy(sub.block_tables),
                                torch.from_numpy(sub.context_lens()), SCALE)
     assert_close(bal[pick], want, f"long decode: sequences {pick} vs oracle")
+
+
+@pytest.mark.parametrize("bs", [16, 32])
+@pytest.mark.parametrize("hq,hkv,part", [(32, 8, 0), (32, 2, 0), (32, 8, 512)])
+def test_decode_small_blocks(bs, hq, hkv, part):
+    """Block sizes 16 and 32 (the reference accepts any kvcache_block_size
+    % 16 == 0): the balanced kernel (32/8), the split-KV kernel chosen by the
+    library (32/2) and forced 512-token partitions, whose 32- or 64-token
+    stages then span several blocks."""
+    rng = np.random.default_rng(bs * 10 + hkv + part)
+    ctx = [1, 15, 16, 17, 31, 32, 33, 63, 64, 65, 300, 1000, 2500] + [int(c) for c in rng.integers(1, 3000, 10)]
+    seqs = [W.SeqSpec(lq=1, cached=c - 1) for c in ctx]
+    wl = W.make_workload(f"small_blocks_{bs}_{hq}_{hkv}", hq, hkv, seqs, seed=int(rng.integers(1 << 30)),
+                         block_size=bs)
+    announce(f"decode: block_size {bs}, {hq}/{hkv} heads, part_tokens {part}")
+    cpu_c, gpu_c = build_pair(wl)
+    q = wl.make_q("cpu")
+    want = _oracle_decode(wl, cpu_c, q)
+    out = _run_decode(wl, gpu_c, q.cuda()) if part == 0 else _forced_split_decode(wl, gpu_c, q.cuda(), part)
+    assert_close(out, want, wl.name)

@@ -39,7 +39,8 @@ def _oracle(wl, cpu_c, q, ctx=None):
     return oa.decode_attention(q, cpu_c[0], cpu_c[1], torch.from_numpy(wl.block_tables), ctx, SCALE)
 
 
-@pytest.mark.parametrize("hq,hkv,bs", [(4, 4, 256), (16, 8, 256), (32, 8, 64), (24, 8, 128), (256, 8, 256)])
+@pytest.mark.parametrize("hq,hkv,bs", [(4, 4, 256), (16, 8, 256), (32, 8, 64), (24, 8, 128), (256, 8, 256),
+                                       (32, 8, 16), (64, 8, 32), (16, 4, 16), (32, 8, 48)])
 def test_balanced_decode_ragged_batch(hq, hkv, bs):
     """Contexts 1..2000 around stage (16) and block boundaries, in random order."""
     rng = np.random.default_rng(hq * 7 + hkv + bs)

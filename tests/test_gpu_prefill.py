@@ -141,11 +141,13 @@ def test_prefill_lq1_equals_decode():
     assert torch.equal(pre, dec), "Lq=1 prefill vs decode"
 
 
-@pytest.mark.parametrize("bs", [64, 192, 512])
+@pytest.mark.parametrize("bs", [16, 32, 48, 64, 192, 512])
 def test_prefill_block_sizes(bs):
-    """Block sizes other than 256 (the block of a tile comes from a multiply
-    with the reciprocal of the tiles per block; 192 is not a power of two);
-    chunks cross many block borders."""
+    """Block sizes other than 256, down to 16 (the reference accepts any
+    kvcache_block_size % 16 == 0): each wave's 8- or 16-row load group gets
+    the block of its first row from a multiply with the reciprocal of the
+    block size; 48 and 192 are not powers of two; with 16 and 32 a 64-token
+    tile spans several blocks.  Chunks cross many block borders."""
     rng = np.random.default_rng(bs)
     seqs = [W.SeqSpec(lq=int(l), cached=int(rng.integers(0, 900))) for l in (300, 129, 64, 7, 512)]
     wl = W.make_workload(f"prefill_bs{bs}", 32, 8, seqs, seed=int(rng.integers(1 << 30)), block_size=bs)
@@ -153,7 +155,7 @@ def test_prefill_block_sizes(bs):
     _check(wl)
 
 
-@pytest.mark.parametrize("bs,cached,lq", [(64, 4500, 300), (256, 16900, 200)])
+@pytest.mark.parametrize("bs,cached,lq", [(16, 2500, 300), (64, 4500, 300), (256, 16900, 200)])
 def test_prefill_multi_window_block_tables(bs, cached, lq):
     """Sequences with more than 64 blocks: the kernel holds a 64-entry window
     of the block table in one register and reloads it at the window edge
@@ -161,6 +163,18 @@ def test_prefill_multi_window_block_tables(bs, cached, lq):
     seqs = [W.SeqSpec(lq=lq, cached=cached), W.SeqSpec(lq=65, cached=4000), W.SeqSpec(lq=33, cached=100)]
     wl = W.make_workload(f"prefill_windows_bs{bs}", 32, 8, seqs, seed=bs + 11, block_size=bs)
     announce(f"prefill: block-table windows, block_size {bs}, Lk {cached + lq}")
+    _check(wl)
+
+
+@pytest.mark.parametrize("bs", [16, 32])
+def test_prefill_small_blocks_split_kv_short_rows(bs):
+    """Block sizes 16 and 32 with 2 kv heads: the short-query rows take the
+    split-KV kernel (its stages span several blocks) and the long ones the
+    prefill kernel, in one call."""
+    rng = np.random.default_rng(bs + 5)
+    seqs = [W.SeqSpec(lq=int(l), cached=int(rng.integers(0, 1500))) for l in (1, 3, 5, 16, 17, 200, 64)]
+    wl = W.make_workload(f"prefill_small_blocks_{bs}", 32, 2, seqs, seed=int(rng.integers(1 << 30)), block_size=bs)
+    announce(f"prefill: block_size {bs}, 32/2 heads (split-KV short rows)")
     _check(wl)
 
 
