@@ -172,14 +172,28 @@ int64_t align_up(int64_t n) { return (n + 255) / 256 * 256; }
 // Prefill kernel geometry for G query heads per kv head.
 int prefill_bm(int g) { return 32 * nvamd::kPrefillWaves / heads_per_workgroup(g); }
 
-constexpr int64_t kPrefillItemBytes = 32;  // sizeof(nvamd::PrefillItem)
+constexpr int64_t kPrefillItemBytes = 48;  // sizeof(nvamd::PrefillItem)
 
-// Bytes of the prefill work list (0 when every sequence takes the
-// short-query path).
-int64_t schedule_bytes(int32_t num_seqs, int g, int32_t max_seqlen_q) {
-  const int mq_max_q = kMqMaxCols / g;
-  if (max_seqlen_q <= mq_max_q) return 0;
-  return (int64_t)num_seqs * ceil_div(max_seqlen_q, prefill_bm(g)) * kPrefillItemBytes;
+// Workspace of the prefill kernel after the short-query partials: the work
+// list, the arrival counters of split items and the partial slots of their
+// pieces (all 0 when every sequence takes the short-query path).
+struct PrefillLayout {
+  int64_t records = 0, slots_per_group = 0, list_bytes = 0, counter_bytes = 0, part_bytes = 0;
+  int64_t bytes() const { return list_bytes + counter_bytes + part_bytes; }
+};
+
+PrefillLayout prefill_layout(int32_t num_seqs, int32_t num_kv_heads, int g, int32_t max_seqlen_q) {
+  PrefillLayout L;
+  if (max_seqlen_q <= kMqMaxCols / g) return L;
+  const int64_t n_items = (int64_t)num_seqs * ceil_div(max_seqlen_q, prefill_bm(g));
+  const int64_t n_groups = (int64_t)num_kv_heads * (g / heads_per_workgroup(g));
+  L.slots_per_group = std::max<int64_t>(1, device_cu_count() / n_groups);
+  L.records = std::max(n_items, 2 * L.slots_per_group);
+  L.list_bytes = align_up(L.records * kPrefillItemBytes);
+  L.counter_bytes = align_up(L.slots_per_group * n_groups * (int64_t)sizeof(int));
+  L.part_bytes = 2 * L.slots_per_group * n_groups * nvamd::kPrefillPartDwords * 64 * nvamd::kPrefillWaves *
+                 (int64_t)sizeof(uint32_t);
+  return L;
 }
 
 }  // namespace
@@ -347,7 +361,7 @@ int64_t nvamd_prefill_workspace_bytes(int64_t num_tokens, int32_t num_seqs, int3
   int64_t partials = partial_bytes(num_tokens, num_heads, ceil_div(kv_cap, part));
   if (block_size > 0 && use_stream_k(num_seqs, num_kv_heads, part_tokens))  // paged: the balanced kernel
     partials = stream_k_bytes(num_seqs, num_kv_heads, G, short_cols(G, max_seqlen_q), true);
-  return align_up(partials) + schedule_bytes(num_seqs, G, max_seqlen_q);
+  return align_up(partials) + prefill_layout(num_seqs, num_kv_heads, G, max_seqlen_q).bytes();
 }
 
 int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, const void* v,
@@ -396,8 +410,8 @@ int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, con
   const bool sk = paged && use_stream_k(num_seqs, num_kv_heads, part_tokens);
   const int64_t partials = sk ? stream_k_bytes(num_seqs, num_kv_heads, G, short_cols(G, max_seqlen_q), true)
                               : partial_bytes(num_tokens, num_heads, ceil_div(kv_cap, part));
-  const int64_t sched = schedule_bytes(num_seqs, G, max_seqlen_q);
-  const int64_t need = align_up(partials) + sched;
+  const PrefillLayout layout = prefill_layout(num_seqs, num_kv_heads, G, max_seqlen_q);
+  const int64_t need = align_up(partials) + layout.bytes();
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
     return fail(NVAMD_ERR_WORKSPACE, "%s: workspace of %lld bytes required (got %lld)", fn,
                 (long long)need, (long long)workspace_bytes);
@@ -471,7 +485,13 @@ int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, con
   pp.blk_magic = (uint32_t)(((1u << 31) - 1u) / (uint32_t)(pp.block_size / 16) + 1u);
   pp.mq_max_q = mq_max_q;
   pp.scale_log2 = softmax_scale * 1.4426950408889634f;
-  void* schedule = static_cast<char*>(workspace) + align_up(partials);
+  char* schedule = static_cast<char*>(workspace) + align_up(partials);
+  if (layout.records > 0x7fffffff / ((int64_t)num_kv_heads * pp.n_hgroups))
+    return fail(NVAMD_ERR_UNSUPPORTED, "%s: too many prefill work items", fn);
+  pp.n_records = (int)layout.records;
+  pp.slots_per_group = (int)layout.slots_per_group;
+  pp.counters = reinterpret_cast<int*>(schedule + layout.list_bytes);
+  pp.part = reinterpret_cast<uint32_t*>(schedule + layout.list_bytes + layout.counter_bytes);
   // The first launch is the short-query pass with one more workgroup that
   // writes the work list: the balanced kernel (one stream-K workgroup fewer,
   // so that the work-list workgroup is resident beside the others) or the

@@ -24,6 +24,9 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+// the vector types of the raw buffer load/store builtins
+typedef unsigned int v4u32_t __attribute__((ext_vector_type(4)));
+typedef unsigned int v2u32_t __attribute__((ext_vector_type(2)));
 
 constexpr int kHeadDim = 128;
 constexpr float kLog2e = 1.4426950408889634f;

@@ -69,7 +69,20 @@ struct PrefillParams {
   uint32_t blk_magic;  // ceil(2^31 / (block_size / 16)): block of key kv = umulhi(2 * (kv >> 4), blk_magic)
   int mq_max_q;   // sequences with Lq <= mq_max_q are left to the short-query kernel
   float scale_log2;
+  // Work list and split key ranges (see prefill_schedule): a call with fewer
+  // items than a round of workgroups splits its long items' tiles into
+  // pieces whose partial results the item's last piece merges.
+  int n_records;        // work-list records: max(num_seqs * n_mblocks, 2 * slots_per_group)
+  int slots_per_group;  // workgroups a kv-head group gets in one round: CUs / (Hkv * n_hgroups), >= 1
+  int* counters;        // [slots_per_group][Hkv * n_hgroups] arrivals per split item and group
+  uint32_t* part;       // [2 * slots_per_group][Hkv * n_hgroups][kPrefillPartDwords][64 * kPrefillWaves]
 };
+
+// Partial result of one lane of a piece of a split item: its 64 accumulators
+// normalised and rounded to fp16 (32 dwords), then m and l.
+constexpr int kPrefillPartDwords = 34;
+// Most pieces one item is split into.
+constexpr int kPrefillMaxPieces = 8;
 
 hipError_t launch_kv_store(const void* key, int64_t key_stride, const void* value,
                            int64_t value_stride, void* k_cache, void* v_cache,
@@ -83,8 +96,6 @@ int decode_sk_wgs_per_cu(int ncb, int hg, int G, bool varlen);
 hipError_t launch_decode_sk(const MqParams& p, int ncb, bool merge, const PrefillParams* pp, void* items,
                             hipStream_t stream);
 
-// Device bytes of the prefill work list (sorted items).
-int64_t prefill_schedule_bytes(const PrefillParams& p);
 
 // Short-query (split-KV) pass of a prefill call whose extra workgroup writes
 // the prefill work list to `items` (prefill_schedule_bytes(pp) bytes).

@@ -594,10 +594,9 @@ __global__ __launch_bounds__(256) void paged_mq_attn_kernel(MqParams p) {
 // workgroup writes the prefill kernel's work list (the prefill kernel is the
 // next launch on the stream).
 template <int NCB, int HG>
-__global__ __launch_bounds__(256) void prefill_short_kernel(MqParams p, PrefillParams pp, PrefillItem* items,
-                                                            int n_items_max) {
+__global__ __launch_bounds__(256) void prefill_short_kernel(MqParams p, PrefillParams pp, PrefillItem* items) {
   if ((int)blockIdx.z == p.num_seqs) {
-    if (blockIdx.x == 0 && blockIdx.y == 0) prefill_schedule(pp, items, n_items_max);
+    if (blockIdx.x == 0 && blockIdx.y == 0) prefill_schedule(pp, items);
     return;
   }
   mq_attn<NCB, HG>(p, blockIdx.x, blockIdx.y, blockIdx.z);
@@ -694,10 +693,9 @@ struct SkStage {
 // sk_wgs, resident beside the sk_wgs stream-K workgroups) that writes the
 // prefill kernel's work list (items != nullptr).
 template <int NCB, int HG, bool QL>
-__global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p, PrefillParams pp, PrefillItem* items,
-                                                            int n_items_max) {
+__global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p, PrefillParams pp, PrefillItem* items) {
   if (items != nullptr && (int)blockIdx.x == p.sk_wgs) {
-    prefill_schedule(pp, items, n_items_max);
+    prefill_schedule(pp, items);
     return;
   }
   using S = SkStage<HG, QL>;
@@ -1093,22 +1091,18 @@ hipError_t launch_decode_sk(const MqParams& p, int ncb, bool merge, const Prefil
   // the work list of a prefill call: one more workgroup
   PrefillParams ppv{};
   PrefillItem* it = nullptr;
-  int n_items = 0;
   if (items != nullptr) {
-    if (pp == nullptr || !varlen) return hipErrorInvalidValue;
-    const int64_t n_items_max = (int64_t)pp->num_seqs * pp->n_mblocks;
-    if (n_items_max > 0x7fffffff) return hipErrorInvalidValue;
+    if (pp == nullptr || !varlen || !schedule_params_ok(*pp)) return hipErrorInvalidValue;
     ppv = *pp;
     it = static_cast<PrefillItem*>(items);
-    n_items = (int)n_items_max;
   }
   const dim3 grid((unsigned)p.sk_wgs + (it != nullptr ? 1u : 0u)), block((unsigned)(64 * hg));
   switch (sk_variant(ncb, hg, p.G, varlen)) {
-    case 0: hipLaunchKernelGGL((decode_sk_kernel<1, 4, false>), grid, block, 0, stream, p, ppv, it, n_items); break;
-    case 1: hipLaunchKernelGGL((decode_sk_kernel<2, 4, false>), grid, block, 0, stream, p, ppv, it, n_items); break;
-    case 2: hipLaunchKernelGGL((decode_sk_kernel<1, 8, true>), grid, block, 0, stream, p, ppv, it, n_items); break;
-    case 3: hipLaunchKernelGGL((decode_sk_kernel<1, 8, false>), grid, block, 0, stream, p, ppv, it, n_items); break;
-    default: hipLaunchKernelGGL((decode_sk_kernel<2, 8, false>), grid, block, 0, stream, p, ppv, it, n_items); break;
+    case 0: hipLaunchKernelGGL((decode_sk_kernel<1, 4, false>), grid, block, 0, stream, p, ppv, it); break;
+    case 1: hipLaunchKernelGGL((decode_sk_kernel<2, 4, false>), grid, block, 0, stream, p, ppv, it); break;
+    case 2: hipLaunchKernelGGL((decode_sk_kernel<1, 8, true>), grid, block, 0, stream, p, ppv, it); break;
+    case 3: hipLaunchKernelGGL((decode_sk_kernel<1, 8, false>), grid, block, 0, stream, p, ppv, it); break;
+    default: hipLaunchKernelGGL((decode_sk_kernel<2, 8, false>), grid, block, 0, stream, p, ppv, it); break;
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -1119,18 +1113,15 @@ hipError_t launch_decode_sk(const MqParams& p, int ncb, bool merge, const Prefil
 
 hipError_t launch_prefill_short(const MqParams& p, int ncb, const PrefillParams& pp, void* items,
                                 hipStream_t stream) {
-  if (p.num_seqs == 0 || items == nullptr) return hipErrorInvalidValue;
-  const int64_t n_items_max = (int64_t)pp.num_seqs * pp.n_mblocks;
-  if (n_items_max > 0x7fffffff) return hipErrorInvalidValue;
+  if (p.num_seqs == 0 || items == nullptr || !schedule_params_ok(pp)) return hipErrorInvalidValue;
   const int hg = (p.Hkv % 2 == 0) ? 2 : 1;  // kv heads per workgroup
   const dim3 grid((unsigned)p.max_parts, (unsigned)(p.Hkv / hg), (unsigned)p.num_seqs + 1u);
   PrefillItem* it = static_cast<PrefillItem*>(items);
-  const int n = (int)n_items_max;
   switch (2 * (ncb - 1) + (hg - 1)) {
-    case 0: hipLaunchKernelGGL((prefill_short_kernel<1, 1>), grid, dim3(256), 0, stream, p, pp, it, n); break;
-    case 1: hipLaunchKernelGGL((prefill_short_kernel<1, 2>), grid, dim3(256), 0, stream, p, pp, it, n); break;
-    case 2: hipLaunchKernelGGL((prefill_short_kernel<2, 1>), grid, dim3(256), 0, stream, p, pp, it, n); break;
-    case 3: hipLaunchKernelGGL((prefill_short_kernel<2, 2>), grid, dim3(256), 0, stream, p, pp, it, n); break;
+    case 0: hipLaunchKernelGGL((prefill_short_kernel<1, 1>), grid, dim3(256), 0, stream, p, pp, it); break;
+    case 1: hipLaunchKernelGGL((prefill_short_kernel<1, 2>), grid, dim3(256), 0, stream, p, pp, it); break;
+    case 2: hipLaunchKernelGGL((prefill_short_kernel<2, 1>), grid, dim3(256), 0, stream, p, pp, it); break;
+    case 3: hipLaunchKernelGGL((prefill_short_kernel<2, 2>), grid, dim3(256), 0, stream, p, pp, it); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

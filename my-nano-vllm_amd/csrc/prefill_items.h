@@ -15,12 +15,15 @@ struct ItemGeom {
   int q_start, Lq, k_start, Lk, c;
 };
 
-// One entry of the prefill work list: a (sequence, m-block) item with its
-// geometry resolved, so that a workgroup needs a single load to start it.
-// seq < 0 marks a slot past the last item.
-// head = {seq, mb, q_start, Lq}, tail = {k_start, Lk, n_tiles, 0}.
+// One entry of the prefill work list: a piece of a (sequence, m-block)
+// item, its geometry resolved so that a workgroup needs a single load to
+// start it.  seq < 0 marks a slot past the last piece.
+// head = {seq, mb, q_start, Lq}, tail = {k_start, Lk, t_lo, t_hi}: tiles
+// [t_lo, t_hi) of the item; split = {piece, pieces, slot, counter}: piece
+// `piece` of `pieces` (1: the whole item), the partial slot of its piece 0
+// (its piece j writes slot + j) and its arrival counter.
 struct PrefillItem {
-  int4 head, tail;
+  int4 head, tail, split;
 };
 
 __device__ __forceinline__ ItemGeom item_geom(const PrefillParams& p, int seq) {
@@ -45,56 +48,139 @@ __device__ __forceinline__ bool item_valid(const PrefillParams& p, const ItemGeo
   return g.Lq > p.mq_max_q && mb * p.BM < g.Lq;
 }
 
-// Work list of the prefill kernel: one workgroup (256 threads or more; the
-// first 256 do the work, the rest only take part in the barriers) writes the
-// (seq, m-block) items in decreasing tile count (counting sort), followed by
-// records with seq = -1 for slots without an item.  Run as an extra
-// workgroup of the launch that precedes the prefill kernel.
-__device__ __forceinline__ void prefill_schedule(const PrefillParams& p, PrefillItem* __restrict__ items,
-                                                 int n_items_max) {
+// Host-side check of the work-list geometry a schedule pass writes.
+inline bool schedule_params_ok(const PrefillParams& p) {
+  const int64_t n_items_max = (int64_t)p.num_seqs * p.n_mblocks;
+  return n_items_max <= 0x7fffffff && p.n_records >= n_items_max && p.n_records >= 2 * p.slots_per_group &&
+         p.slots_per_group >= 1 && p.counters != nullptr && p.part != nullptr;
+}
+
+// Pieces item of n tiles is split into when its call splits (piece_tiles
+// > 0): about n / piece_tiles, at least 2 tiles each, at most
+// kPrefillMaxPieces.
+__device__ __forceinline__ int item_pieces(int n, int piece_tiles) {
+  if (piece_tiles <= 0 || n < 4) return 1;
+  return max(1, min(min((n + piece_tiles - 1) / piece_tiles, n / 2), kPrefillMaxPieces));
+}
+
+// Tiles [lo, hi) of piece j of k over n tiles (sizes differ by at most 1).
+__device__ __forceinline__ int piece_lo(int n, int k, int j) { return j * n / k; }
+
+// Inclusive scan over the 256 worker threads (4 waves); warp_tot holds 4 ints.
+__device__ __forceinline__ int block_incl_scan(int x, int* warp_tot, int& total) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int incl = x;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += o;
+  }
+  if (tid < 256 && lane == 63) warp_tot[wave] = incl;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wave && w < 4; ++w) base += warp_tot[w];
+  total = warp_tot[0] + warp_tot[1] + warp_tot[2] + warp_tot[3];
+  __syncthreads();
+  return base + incl;
+}
+
+// Work list of the prefill kernel, written by one workgroup (256 threads or
+// more; the first 256 do the work, the rest only take part in the
+// barriers) run as an extra workgroup of the launch that precedes the
+// prefill kernel.
+//
+// Items are the valid (sequence, m-block) pairs.  When there are fewer
+// than a round of workgroups' worth of them (V < slots_per_group per
+// kv-head group), long items are split into pieces of about T / slots_per_group
+// tiles (T = all items' tiles), lengthened until the pieces fit one round,
+// so the pieces fill the machine and the longest one is short; a split
+// item gets consecutive partial slots and an arrival counter (zeroed here,
+// so the prefill kernel, the next launch, starts from zero).  The pieces
+// are written in decreasing tile count (counting sort), followed by records
+// with seq = -1 up to n_records.  Each thread keeps the geometry of its
+// first kSchedCached candidates in registers, so the passes over the items
+// read the sequence lengths from memory once.
+constexpr int kSchedCached = 4;
+
+__device__ __forceinline__ void prefill_schedule(const PrefillParams& p, PrefillItem* __restrict__ items) {
   __shared__ int hist[kCostBuckets];
   __shared__ int warp_tot[4];
   const int tid = threadIdx.x;
   const bool worker = tid < 256;
-  const int lane = tid & 63, wave = tid >> 6;
-  if (worker)
+  const int n_items_max = p.num_seqs * p.n_mblocks;
+  const int n_groups = p.Hkv * p.n_hgroups;
+  if (worker) {
     for (int b = tid; b < kCostBuckets; b += 256) hist[b] = 0;
-  __syncthreads();
-  if (worker)
-    for (int idx = tid; idx < n_items_max; idx += 256) {
-      const int seq = idx / p.n_mblocks, mb = idx - seq * p.n_mblocks;
-      const ItemGeom g = item_geom(p, seq);
-      if (!item_valid(p, g, mb)) continue;
-      atomicAdd(&hist[min(item_tiles(p, g, mb), kCostBuckets - 1)], 1);
+    for (int c = tid; c < p.slots_per_group * n_groups; c += 256) p.counters[c] = 0;
+  }
+  // candidate idx: its geometry and tile count (-1: not a valid item)
+  auto candidate = [&](int idx, ItemGeom& g) {
+    const int seq = idx / p.n_mblocks, mb = idx - seq * p.n_mblocks;
+    g = item_geom(p, seq);
+    return item_valid(p, g, mb) ? item_tiles(p, g, mb) : -1;
+  };
+  ItemGeom cg[kSchedCached];
+  int ct[kSchedCached];
+#pragma unroll
+  for (int i = 0; i < kSchedCached; ++i) {
+    const int idx = tid + 256 * i;
+    cg[i] = ItemGeom{};
+    ct[i] = (worker && idx < n_items_max) ? candidate(idx, cg[i]) : -1;
+  }
+  // f(tiles, geometry, idx) for this thread's valid candidates: the cached
+  // ones (static indices, so they stay in registers), then the rest
+  auto each_item = [&](auto&& f) {
+    if (!worker) return;
+#pragma unroll
+    for (int i = 0; i < kSchedCached; ++i)
+      if (ct[i] >= 0) f(ct[i], cg[i], tid + 256 * i);
+    for (int idx = tid + 256 * kSchedCached; idx < n_items_max; idx += 256) {
+      ItemGeom g;
+      const int n = candidate(idx, g);
+      if (n >= 0) f(n, g, idx);
     }
+  };
+  // valid items and their tiles
+  int v = 0, tt = 0;
+  each_item([&](int n, const ItemGeom&, int) {
+    ++v;
+    tt += n;
+  });
+  int n_valid = 0, n_tiles_all = 0;
+  block_incl_scan(v, warp_tot, n_valid);
+  block_incl_scan(tt, warp_tot, n_tiles_all);
+  const bool split = n_valid > 0 && n_valid < p.slots_per_group;
+  // piece length: from T / slots_per_group up, until the pieces fit one round
+  int piece_tiles = split ? max(2, (n_tiles_all + p.slots_per_group - 1) / p.slots_per_group) : 0;
+  for (int iter = 0; split && iter < 16; ++iter) {
+    int np = 0;
+    each_item([&](int n, const ItemGeom&, int) { np += item_pieces(n, piece_tiles); });
+    int n_pieces = 0;
+    block_incl_scan(np, warp_tot, n_pieces);
+    if (n_pieces <= p.slots_per_group) break;
+    piece_tiles += max(1, piece_tiles / 4);
+  }
+  // histogram of piece sizes
+  each_item([&](int n, const ItemGeom&, int) {
+    const int k = item_pieces(n, piece_tiles);
+    for (int j = 0; j < k; ++j)
+      atomicAdd(&hist[min(piece_lo(n, k, j + 1) - piece_lo(n, k, j), kCostBuckets - 1)], 1);
+  });
   __syncthreads();
   // Exclusive scan in decreasing cost order: thread t owns buckets
   // [1023 - 4t - 3, 1023 - 4t] (walked from high cost to low).
-  int local[4] = {0, 0, 0, 0}, sum = 0, incl = 0;
+  int local[4] = {0, 0, 0, 0}, sum = 0;
   if (worker) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       local[j] = hist[kCostBuckets - 1 - (4 * tid + j)];
       sum += local[j];
     }
-    incl = sum;  // inclusive scan of per-thread sums over the wave
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int o = __shfl_up(incl, off, 64);
-      if (lane >= off) incl += o;
-    }
-    if (lane == 63) warp_tot[wave] = incl;
   }
-  __syncthreads();
-  int total = 0, run = 0;
+  int total = 0;
+  const int incl = block_incl_scan(sum, warp_tot, total);
   if (worker) {
-    int base = 0;
-    for (int w = 0; w < wave; ++w) base += warp_tot[w];
-    total = warp_tot[0] + warp_tot[1] + warp_tot[2] + warp_tot[3];
-    run = base + incl - sum;
-  }
-  __syncthreads();
-  if (worker) {
+    int run = incl - sum;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       hist[kCostBuckets - 1 - (4 * tid + j)] = run;
@@ -102,17 +188,38 @@ __device__ __forceinline__ void prefill_schedule(const PrefillParams& p, Prefill
     }
   }
   __syncthreads();
-  if (!worker) return;
-  for (int idx = tid; idx < n_items_max; idx += 256) {
+  // Scatter the pieces; split items take partial slots and counters in item
+  // order (a scan over the candidates, 256 at a time: round i covers
+  // candidates [256 i, 256 i + 256)).
+  int slot_carry = 0, cnt_carry = 0;
+  auto scatter_round = [&](int n, const ItemGeom& g, int idx) {
+    const int k = n >= 0 ? item_pieces(n, piece_tiles) : 0;
+    const int ks = k > 1 ? k : 0;
+    int slots_total = 0, cnt_total = 0;
+    const int slot0 = slot_carry + block_incl_scan(ks, warp_tot, slots_total) - ks;
+    const int cnt0 = cnt_carry + block_incl_scan(ks > 0 ? 1 : 0, warp_tot, cnt_total) - (ks > 0 ? 1 : 0);
+    slot_carry += slots_total;
+    cnt_carry += cnt_total;
     const int seq = idx / p.n_mblocks, mb = idx - seq * p.n_mblocks;
-    const ItemGeom g = item_geom(p, seq);
-    if (!item_valid(p, g, mb)) continue;
-    const int tiles = item_tiles(p, g, mb);
-    const int pos = atomicAdd(&hist[min(tiles, kCostBuckets - 1)], 1);
-    items[pos] = PrefillItem{make_int4(seq, mb, g.q_start, g.Lq), make_int4(g.k_start, g.Lk, tiles, 0)};
+    for (int j = 0; j < k; ++j) {
+      const int lo = piece_lo(n, k, j), hi = piece_lo(n, k, j + 1);
+      const int pos = atomicAdd(&hist[min(hi - lo, kCostBuckets - 1)], 1);
+      items[pos] = PrefillItem{make_int4(seq, mb, g.q_start, g.Lq), make_int4(g.k_start, g.Lk, lo, hi),
+                               make_int4(j, k, k > 1 ? slot0 : -1, k > 1 ? cnt0 : -1)};
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < kSchedCached; ++i)
+    if (256 * i < n_items_max) scatter_round(worker ? ct[i] : -1, cg[i], tid + 256 * i);
+  for (int base = 256 * kSchedCached; base < n_items_max; base += 256) {
+    const int idx = base + tid;
+    ItemGeom g{};
+    const int n = (worker && idx < n_items_max) ? candidate(idx, g) : -1;
+    scatter_round(n, g, idx);
   }
-  for (int pos = total + tid; pos < n_items_max; pos += 256)
-    items[pos] = PrefillItem{make_int4(-1, 0, 0, 0), make_int4(0, 0, 0, 0)};
+  if (worker)
+    for (int pos = total + tid; pos < p.n_records; pos += 256)
+      items[pos] = PrefillItem{make_int4(-1, 0, 0, 0), make_int4(0, 0, 0, 0), make_int4(0, 1, -1, -1)};
 }
 
 }  // namespace nvamd

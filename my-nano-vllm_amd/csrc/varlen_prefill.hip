@@ -133,16 +133,19 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
     return;
   }
 
-  // blockIdx.x = item * n_groups + group: the kv-head group varies fastest.
+  // blockIdx.x = record * n_groups + group: the kv-head group varies fastest.
   const int n_groups = p.Hkv * p.n_hgroups;
   const int item = (int)(blockIdx.x / (unsigned)n_groups);
   const int grp = (int)blockIdx.x - item * n_groups;
-  // one record load gives the item and its geometry
-  const int4 rec_a = items[item].head, rec_b = items[item].tail;
+  // one record load gives the piece and its geometry
+  const int4 rec_a = items[item].head, rec_b = items[item].tail, rec_c = items[item].split;
   const int seq = wave_uniform(rec_a.x);
   if (seq < 0) return;
   const int mb = wave_uniform(rec_a.y), q_start = wave_uniform(rec_a.z), Lq = wave_uniform(rec_a.w);
-  const int k_start = wave_uniform(rec_b.x), Lk = wave_uniform(rec_b.y), n_tiles = wave_uniform(rec_b.z);
+  const int k_start = wave_uniform(rec_b.x), Lk = wave_uniform(rec_b.y);
+  const int t_lo = wave_uniform(rec_b.z), n_tiles = wave_uniform(rec_b.w);  // this piece: tiles [t_lo, n_tiles)
+  const int piece = wave_uniform(rec_c.x), n_pieces = wave_uniform(rec_c.y);
+  const int part_slot = wave_uniform(rec_c.z), counter = wave_uniform(rec_c.w);
   const int c = Lk - Lq;
   const int g = grp / p.n_hgroups;
   const int hg = grp - g * p.n_hgroups;
@@ -500,13 +503,16 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
   uint16_t* kbuf1 = lds + kKElems;
   uint16_t* vbuf0 = lds + 2 * kKElems;
   uint16_t* vbuf1 = vbuf0 + kVElems;
-  const int win_tiles = PAGED ? kBtWindow * p.block_size / kBN : n_tiles;
+  // Window w holds the blocks of tiles [w * win_tiles, (w + 1) * win_tiles);
+  // a piece starts inside one and ends inside one.
+  const int win_tiles = PAGED ? kBtWindow * p.block_size / kBN : max(n_tiles, 1);
   // The tile loop, specialised for the wave's role (K or V staging).
   auto tile_loop = [&](auto role) {
-  for (int t0 = 0; t0 < n_tiles; t0 += win_tiles) {
-    const int t1 = min(n_tiles, t0 + win_tiles);
+  for (int t0 = t_lo, t1; t0 < n_tiles; t0 = t1) {
+    const int win = t0 / win_tiles;
+    t1 = min(n_tiles, (win + 1) * win_tiles);
     if constexpr (PAGED) {
-      win_base = (t0 * kBN) / p.block_size;
+      win_base = win * kBtWindow;
       const int bi = min(win_base + lane, (int)p.bt_stride - 1);
       const int blk = p.block_tables[(int64_t)seq * p.bt_stride + bi];
       const int64_t row = (int64_t)blk * p.block_size;
@@ -602,6 +608,102 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
 
   // ---- normalise and store ----------------------------------------------------
   l_run += shfl_xor_f32(l_run, 32);
+  if (n_pieces > 1) {
+    // A piece of a split item: write this lane's partial (accumulators
+    // normalised, fp16; m, l) to the piece's slot; the item's last piece to
+    // arrive merges all pieces, in piece order, and stores the output.  The
+    // partials are written and read with agent-coherent buffer accesses
+    // (sc1: coherent across the XCDs' L2 caches without writing back or
+    // invalidating them), and each wave's stores have completed before the
+    // arrival is counted.
+    constexpr int kLanes = 64 * kPrefillWaves;
+    constexpr int kSc1 = 16;  // cache-policy bit sc1 of a buffer access
+    const uint32_t slot_bytes = (uint32_t)(kPrefillPartDwords * kLanes * 4);
+    const uint32_t piece_stride = (uint32_t)n_groups * slot_bytes;
+    const __amdgpu_buffer_rsrc_t pr =
+        make_rsrc(p.part + ((int64_t)part_slot * n_groups + grp) * (kPrefillPartDwords * kLanes),
+                  (uint32_t)n_pieces * piece_stride);
+    {
+      const float inv = (l_run > 0.f) ? 1.0f / l_run : 0.f;
+      const uint32_t mine = (uint32_t)piece * piece_stride;
+#pragma unroll
+      for (int w4 = 0; w4 < 8; ++w4) {  // dwords 4 w4 .. 4 w4 + 3: accumulators 8 w4 .. 8 w4 + 7
+        const int db = w4 >> 1, i0 = 8 * (w4 & 1);
+        const u32x4 hv = {pack_f16x2(acc[db][i0 + 0] * inv, acc[db][i0 + 1] * inv),
+                          pack_f16x2(acc[db][i0 + 2] * inv, acc[db][i0 + 3] * inv),
+                          pack_f16x2(acc[db][i0 + 4] * inv, acc[db][i0 + 5] * inv),
+                          pack_f16x2(acc[db][i0 + 6] * inv, acc[db][i0 + 7] * inv)};
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u32_t, hv), pr,
+                                               (int)(mine + 16u * (uint32_t)(w4 * kLanes + tid)), 0, kSc1);
+      }
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32_t, f32x2{m_run, l_run}), pr,
+                                            (int)(mine + 32u * 4u * kLanes + 8u * (uint32_t)tid), 0, kSc1);
+    }
+    __shared__ int s_last;
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores have completed
+    __syncthreads();
+    if (tid == 0) {
+      const int arrived = __hip_atomic_fetch_add(p.counters + (int64_t)counter * n_groups + grp, 1, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+      s_last = (arrived == n_pieces - 1) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    // (m, l) of every piece in one round trip, then the pieces' accumulators
+    // with the next piece's loads in flight while one is added
+    auto ml_off = [&](int j) { return (int)((uint32_t)j * piece_stride + 32u * 4u * kLanes + 8u * (uint32_t)tid); };
+    auto acc_off = [&](int j, int w4) { return (int)((uint32_t)j * piece_stride + 16u * (uint32_t)(w4 * kLanes + tid)); };
+    float mj[kPrefillMaxPieces], lj[kPrefillMaxPieces];
+#pragma unroll
+    for (int j = 0; j < kPrefillMaxPieces; ++j) {
+      const f32x2 ml = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(pr, ml_off(min(j, n_pieces - 1)),
+                                                                                     0, kSc1));
+      mj[j] = (j < n_pieces) ? ml.x : -INFINITY;
+      lj[j] = (j < n_pieces) ? ml.y : 0.f;
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kPrefillMaxPieces; ++j) M = fmaxf(M, mj[j]);
+    const float Ms = (M == -INFINITY) ? 0.f : M;
+    float L = 0.f;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) acc[db] = f32x16{};
+    u32x4 nxt[8];
+#pragma unroll
+    for (int w4 = 0; w4 < 8; ++w4)
+      nxt[w4] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, acc_off(0, w4), 0, kSc1));
+    for (int j = 0; j < n_pieces; ++j) {
+      u32x4 cur[8];
+#pragma unroll
+      for (int w4 = 0; w4 < 8; ++w4) cur[w4] = nxt[w4];
+      if (j + 1 < n_pieces) {
+#pragma unroll
+        for (int w4 = 0; w4 < 8; ++w4)
+          nxt[w4] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, acc_off(j + 1, w4), 0, kSc1));
+      }
+      float mjj = mj[0], ljj = lj[0];
+#pragma unroll
+      for (int q = 1; q < kPrefillMaxPieces; ++q) {
+        mjj = (q == j) ? mj[q] : mjj;
+        ljj = (q == j) ? lj[q] : ljj;
+      }
+      const float wj = (mjj == -INFINITY) ? 0.f : ljj * fast_exp2(mjj - Ms);
+      L += wj;
+#pragma unroll
+      for (int w4 = 0; w4 < 8; ++w4) {
+        const u32x4 hv = cur[w4];
+        const int db = w4 >> 1, i0 = 8 * (w4 & 1);
+        const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const f16x2 h2 = __builtin_bit_cast(f16x2, hw[e]);
+          acc[db][i0 + 2 * e] += wj * (float)h2.x;
+          acc[db][i0 + 2 * e + 1] += wj * (float)h2.y;
+        }
+      }
+    }
+    l_run = L;
+  }
   const int64_t row = (int64_t)q_start + tq;
   if (tq < Lq && row < p.q_rows) {
     const float inv = (l_run > 0.f) ? 1.0f / l_run : 0.f;
@@ -620,17 +722,15 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
   }
 }
 
-static_assert(sizeof(PrefillItem) == 32, "the host sizes the work list with 32-byte records");
-
-int64_t prefill_schedule_bytes(const PrefillParams& p) {
-  return (int64_t)p.num_seqs * p.n_mblocks * (int64_t)sizeof(PrefillItem);
-}
+static_assert(sizeof(PrefillItem) == 48, "the host sizes the work list with 48-byte records");
 
 hipError_t launch_varlen_prefill(const PrefillParams& p, const void* schedule, const MqParams& mq, bool merge,
                                  hipStream_t stream) {
   if (p.num_seqs == 0 || p.n_mblocks == 0) return hipSuccess;
-  const int64_t n_items_max = (int64_t)p.num_seqs * p.n_mblocks;
-  const int64_t n_blocks = n_items_max * p.Hkv * p.n_hgroups;
+  if (p.n_records < (int64_t)p.num_seqs * p.n_mblocks || p.slots_per_group < 1 || p.counters == nullptr ||
+      p.part == nullptr)
+    return hipErrorInvalidValue;
+  const int64_t n_blocks = (int64_t)p.n_records * p.Hkv * p.n_hgroups;
   const int64_t n_merge = merge ? (int64_t)mq.num_seqs * merge_slices(mq, kPrefillWaves) : 0;
   if (n_blocks + n_merge > 0x7fffffff || schedule == nullptr) return hipErrorInvalidValue;
   const dim3 grid((unsigned)(n_blocks + n_merge)), block(64 * kPrefillWaves);

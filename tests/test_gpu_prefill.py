@@ -178,6 +178,31 @@ def test_prefill_small_blocks_split_kv_short_rows(bs):
     _check(wl)
 
 
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (8, 8), (16, 2)])
+def test_prefill_split_pieces_both_layouts(hq, hkv):
+    """Calls with fewer work items than a round of workgroups split their long
+    items' key ranges into pieces merged by the item's last piece: a
+    2048-token prompt (pieces cross the causal diagonal of every m-block
+    near the end), a 700-token chunk over 1000 cached keys and a short chunk,
+    in the paged layout and in the contiguous one (the same K/V rows
+    gathered), against the oracle."""
+    seqs = [W.SeqSpec(lq=2048, cached=0), W.SeqSpec(lq=700, cached=1000), W.SeqSpec(lq=40, cached=90)]
+    wl = W.make_workload(f"prefill_split_{hq}_{hkv}", hq, hkv, seqs, seed=hq * 7 + hkv)
+    announce(f"prefill: split key ranges, {hq}/{hkv} heads, paged and contiguous")
+    cpu_c, gpu_c, q, paged_out = _check(wl)
+    rows = np.concatenate([wl.slots_for(i, 0, s.lk) for i, s in enumerate(wl.seqs)]).astype(np.int64)
+    idx = torch.from_numpy(rows).cuda()
+    kcont = gpu_c[0].view(torch.uint8).reshape(-1, hkv, 128)[idx].view(torch.float8_e4m3fn)
+    vcont = gpu_c[1].view(torch.uint8).reshape(-1, hkv, 128)[idx].view(torch.float8_e4m3fn)
+    out = _prefill_gpu(wl, gpu_c, q.cuda(), paged=False, kv=(kcont, vcont))
+    cu_q, cu_k = wl.cu_seqlens()
+    want = oa.prefill_attention(q, kcont.cpu(), vcont.cpu(), None, torch.from_numpy(cu_q),
+                                torch.from_numpy(cu_k), SCALE)
+    assert_close(out, want, "contiguous, split pieces")
+    again = _prefill_gpu(wl, gpu_c, q.cuda(), paged=False, kv=(kcont, vcont))
+    assert torch.equal(out, again), "split pieces: the merge order is fixed, so repeated calls are bit-identical"
+
+
 def test_prefill_outlier_kv():
     """1 % of the K/V entries scaled by 20 before quantisation (peaked scores,
     values near the E4M3 range): the lazy rescale and the bf16 weights stay
