@@ -24,6 +24,8 @@ Secondary fields in the same JSON line:
                context U[32K, 128K], 1% of K/V x20);
   store        the KV store/quantise of the prefill workload's 8192 new
                tokens (strided K/V views of a fused qkv tensor), GB/s;
+  qk_norm_rope_store  the fused q/k RMSNorm + RoPE + FP8 KV store of the
+               same tokens (QKV projection output in, q and cache rows out), GB/s;
   mixed        the mixed batch's varlen call (32 speculative x 5 rows + 3 x
                512-token chunks, Qwen3-8B shapes), TFLOP/s, and its
                speculative rows alone, GB/s over their decode bytes;
@@ -196,6 +198,34 @@ def bench_store(wl, steps, warmup, n_src=6):
 
     ms = timed(step, steps, warmup, SECONDARY_WARM_S)
     nbytes = n * hkv * 128 * (2 * 2 + 2) + 4 * n
+    return dict(ms=ms, bytes=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9)
+
+
+def bench_qk_norm_rope(wl, steps, warmup, n_src=6):
+    """Fused q/k RMSNorm + RoPE + FP8 KV store of the workload's new tokens:
+    the projection output [N, (Hq + 2 Hkv) * 128] bf16 in, q bf16 and the
+    FP8 K/V cache rows out; n_src projection outputs rotate so the reads
+    come from HBM.  Algorithmic bytes: qkv read, positions, slot ids, one
+    fp32 cos/sin row per token, q written, FP8 K and V written."""
+    from nanovllm_amd.layers.qk_norm_rope import qk_norm_rope_store
+    n = wl.num_q_tokens()
+    hq, hkv = wl.num_heads, wl.num_kv_heads
+    slots = torch.from_numpy(wl.new_token_slots()).cuda()
+    positions = torch.from_numpy(np.concatenate([np.arange(s.cached, s.lk) for s in wl.seqs])).cuda()
+    kc, vc = wl.empty_caches("cuda")
+    g = torch.Generator(device="cuda").manual_seed(wl.seed)
+    srcs = [torch.randn(n, (hq + 2 * hkv) * 128, generator=g, device="cuda").to(torch.bfloat16) for _ in range(n_src)]
+    wq = (1.0 + 0.1 * torch.randn(128, generator=g, device="cuda")).to(torch.bfloat16)
+    wk = (1.0 + 0.1 * torch.randn(128, generator=g, device="cuda")).to(torch.bfloat16)
+    inv_freq = 1.0 / (1e6 ** (torch.arange(0, 128, 2, dtype=torch.float32, device="cuda") / 128))
+    ang = torch.outer(torch.arange(40960, dtype=torch.float32, device="cuda"), inv_freq)
+    cos_sin = torch.cat((ang.cos(), ang.sin()), dim=-1)
+
+    def step(i):
+        qk_norm_rope_store(positions, srcs[i % n_src], wq, wk, 1e-6, cos_sin, kc, vc, slots, hq, hkv)
+
+    ms = timed(step, steps, warmup, SECONDARY_WARM_S)
+    nbytes = n * ((hq + 2 * hkv) * 128 * 2 + 8 + 4 + 128 * 4 + hq * 128 * 2 + 2 * hkv * 128)
     return dict(ms=ms, bytes=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9)
 
 
@@ -413,6 +443,16 @@ def main():
                               ms_per_step=round(res["ms"], 5), gbs=round(res["gbs"], 2),
                               frac_hbm_peak=round(res["gbs"] / HBM_PEAK_GBS, 4), algorithmic_bytes_per_step=res["bytes"],
                               kernels="kv_store_fp8_kernel")
+        torch.cuda.empty_cache()
+
+    if args.only in ("store", "all"):
+        wl = W.qwen3_8b_prefill()
+        res = bench_qk_norm_rope(wl, max(args.steps, 20), max(args.warmup, 5))
+        log(f"fused q/k norm + rope + store: {res['ms'] * 1e3:.1f} us/step, {res['gbs']:.1f} GB/s")
+        extra["qk_norm_rope_store"] = dict(
+            workload=wl.name + " new tokens (8192 x (32 + 2 x 8) head rows of the QKV projection output)",
+            ms_per_step=round(res["ms"], 5), gbs=round(res["gbs"], 2), frac_hbm_peak=round(res["gbs"] / HBM_PEAK_GBS, 4),
+            algorithmic_bytes_per_step=res["bytes"], kernels="qk_norm_rope_store_kernel")
         torch.cuda.empty_cache()
 
     if args.only in ("mixed", "all"):

@@ -11,6 +11,8 @@
  *                                   (wrapper fp8_decode_attention,         nanovllm/kernels/fp8_attention.py:173-207)
  *   nvamd_fp8_prefill_attention  <- fp8_paged_attention_prefill_kernel[grid] nanovllm/kernels/fp8_attention.py:341-352
  *                                   (wrapper fp8_prefill_attention,        nanovllm/kernels/fp8_attention.py:314-353)
+ *   nvamd_qk_norm_rope_store     <- q_norm, k_norm, rotary_emb, store_kvcache  nanovllm/models/qwen3.py:107-110,
+ *                                   nanovllm/layers/attention.py:61-62
  *
  * Conventions
  *   - All pointers are device pointers (HIP), except where noted.  No call
@@ -47,7 +49,7 @@ extern "C" {
 #define NVAMD_ERR_LAUNCH 4
 
 /* ABI version of this header (bumped on any signature change). */
-#define NVAMD_ABI_VERSION 3
+#define NVAMD_ABI_VERSION 4
 int32_t nvamd_abi_version(void);
 
 /* Description of the last error on the calling thread ("" if none). */
@@ -71,6 +73,34 @@ int32_t nvamd_store_kvcache(const void* key, int64_t key_stride0,
                             const int32_t* slot_mapping, int64_t num_tokens,
                             int32_t num_kv_heads, int32_t head_dim, int64_t num_slots,
                             void* stream);
+
+/*
+ * Fused q/k RMSNorm + rotary embedding + FP8 KV store of one attention
+ * layer.  Replaces, between the QKV projection and the attention call, the
+ * q_norm / k_norm RMSNorm (nanovllm/models/qwen3.py:107-109,
+ * nanovllm/layers/layernorm.py:16-25), the rotary embedding (qwen3.py:110,
+ * nanovllm/layers/rotary_embedding.py:40-50) and the KV store
+ * (nanovllm/layers/attention.py:61-62).
+ *
+ * qkv: bf16 [num_tokens, (num_heads + 2 num_kv_heads) * head_dim], row
+ *   stride qkv_stride0 elements (the projection output; q, k, v columns).
+ * positions: int64 [num_tokens]; values outside [0, max_position) read the
+ *   nearest row of the table.
+ * q_norm_weight / k_norm_weight: bf16 [head_dim].
+ * cos_sin_cache: fp32 [max_position, head_dim] (cos of the head_dim/2
+ *   frequencies, then sin; the reference's cos_sin_cache without its unit dim).
+ * q_out: bf16 [num_tokens, num_heads, head_dim] = RoPE(RMSNorm(q)).
+ * k_out: bf16 [num_tokens, num_kv_heads, head_dim] = RoPE(RMSNorm(k)), or NULL.
+ * k_cache / v_cache, slot_mapping, num_slots: as nvamd_store_kvcache; the
+ *   cache receives E4M3FN(RoPE(RMSNorm(k))) and E4M3FN(v).
+ * head_dim must be 128; tensors 16-byte aligned (caches 8).
+ */
+int32_t nvamd_qk_norm_rope_store(const void* qkv, int64_t qkv_stride0, const int64_t* positions,
+                                 const void* q_norm_weight, const void* k_norm_weight, float eps,
+                                 const float* cos_sin_cache, int64_t max_position, void* q_out, void* k_out,
+                                 void* k_cache, void* v_cache, const int32_t* slot_mapping, int64_t num_tokens,
+                                 int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int64_t num_slots,
+                                 void* stream);
 
 /* Workspace needed by nvamd_fp8_decode_attention for these static shapes
  * (part_tokens = 0 selects the library's partition size). */

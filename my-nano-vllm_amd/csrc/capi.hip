@@ -224,6 +224,53 @@ int32_t nvamd_store_kvcache(const void* key, int64_t key_stride0, const void* va
                        "store_kvcache");
 }
 
+int32_t nvamd_qk_norm_rope_store(const void* qkv, int64_t qkv_stride0, const int64_t* positions,
+                                 const void* q_norm_weight, const void* k_norm_weight, float eps,
+                                 const float* cos_sin_cache, int64_t max_position, void* q_out, void* k_out,
+                                 void* k_cache, void* v_cache, const int32_t* slot_mapping, int64_t num_tokens,
+                                 int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int64_t num_slots,
+                                 void* stream) {
+  static const char* fn = "qk_norm_rope_store";
+  if (head_dim != kHeadDim)
+    return fail(NVAMD_ERR_UNSUPPORTED, "%s: head_dim must be %d (got %d)", fn, kHeadDim, head_dim);
+  if (num_tokens < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_slots < 0 || max_position <= 0)
+    return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: bad sizes (N=%lld Hq=%d Hkv=%d slots=%lld max_position=%lld)", fn,
+                (long long)num_tokens, num_heads, num_kv_heads, (long long)num_slots, (long long)max_position);
+  if (!(eps >= 0.f) || !std::isfinite(eps))
+    return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: eps must be finite and non-negative", fn);
+  if (qkv_stride0 < (int64_t)(num_heads + 2 * num_kv_heads) * head_dim)
+    return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: qkv row stride %lld is shorter than a row", fn, (long long)qkv_stride0);
+  if (num_tokens == 0) return ok();
+  if (!qkv || !positions || !q_norm_weight || !k_norm_weight || !cos_sin_cache || !q_out || !k_cache || !v_cache ||
+      !slot_mapping)
+    return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+  if (qkv_stride0 % 8 != 0 || (uintptr_t)qkv % 16 != 0 || (uintptr_t)q_out % 16 != 0 ||
+      (k_out && (uintptr_t)k_out % 16 != 0) || (uintptr_t)q_norm_weight % 16 != 0 ||
+      (uintptr_t)k_norm_weight % 16 != 0 || (uintptr_t)cos_sin_cache % 16 != 0 || (uintptr_t)k_cache % 8 != 0 ||
+      (uintptr_t)v_cache % 8 != 0)
+    return fail(NVAMD_ERR_UNSUPPORTED, "%s: tensors must be 16-byte aligned (caches 8) with a row stride of 8 elements",
+                fn);
+  nvamd::QkNormRopeParams p{};
+  p.qkv = static_cast<const uint16_t*>(qkv);
+  p.qkv_stride = qkv_stride0;
+  p.positions = positions;
+  p.q_weight = static_cast<const uint16_t*>(q_norm_weight);
+  p.k_weight = static_cast<const uint16_t*>(k_norm_weight);
+  p.cos_sin = cos_sin_cache;
+  p.max_position = max_position;
+  p.slot_mapping = slot_mapping;
+  p.k_cache = static_cast<uint8_t*>(k_cache);
+  p.v_cache = static_cast<uint8_t*>(v_cache);
+  p.num_slots = num_slots;
+  p.q_out = static_cast<uint16_t*>(q_out);
+  p.k_out = static_cast<uint16_t*>(k_out);
+  p.num_tokens = num_tokens;
+  p.Hq = num_heads;
+  p.Hkv = num_kv_heads;
+  p.eps = eps;
+  return launch_status(nvamd::launch_qk_norm_rope_store(p, (hipStream_t)stream), fn);
+}
+
 int64_t nvamd_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t num_kv_heads,
                                      int32_t max_num_blocks, int32_t block_size, int32_t part_tokens) {
   if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || max_num_blocks <= 0 || block_size <= 0)

@@ -84,6 +84,28 @@ constexpr int kPrefillPartDwords = 34;
 // Most pieces one item is split into.
 constexpr int kPrefillMaxPieces = 8;
 
+// Fused q/k RMSNorm + rotary embedding + FP8 KV store (qk_norm_rope.hip).
+struct QkNormRopeParams {
+  const uint16_t* qkv;        // bf16 [num_tokens, (Hq + 2 Hkv) * 128], row stride qkv_stride elements
+  int64_t qkv_stride;
+  const int64_t* positions;   // [num_tokens]
+  const uint16_t* q_weight;   // bf16 [128]
+  const uint16_t* k_weight;   // bf16 [128]
+  const float* cos_sin;       // fp32 [max_position, 128]: cos of the 64 frequencies, then sin
+  int64_t max_position;
+  const int32_t* slot_mapping;  // [num_tokens]; -1 stores nothing
+  uint8_t* k_cache;           // E4M3FN [num_slots, Hkv * 128]
+  uint8_t* v_cache;
+  int64_t num_slots;
+  uint16_t* q_out;            // bf16 [num_tokens, Hq, 128]
+  uint16_t* k_out;            // bf16 [num_tokens, Hkv, 128] or nullptr
+  int64_t num_tokens;
+  int Hq, Hkv;
+  float eps;
+};
+
+hipError_t launch_qk_norm_rope_store(const QkNormRopeParams& p, hipStream_t stream);
+
 hipError_t launch_kv_store(const void* key, int64_t key_stride, const void* value,
                            int64_t value_stride, void* k_cache, void* v_cache,
                            const int32_t* slot_mapping, int64_t num_tokens, int row_elems,

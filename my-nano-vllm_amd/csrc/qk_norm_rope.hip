@@ -1,0 +1,144 @@
+// Fused q/k RMSNorm + rotary embedding + FP8 KV store for gfx950.
+//
+// Replaces, for one attention layer, the steps between the QKV projection
+// and the attention call: the q/k RMSNorm (nanovllm/models/qwen3.py:107-109,
+// nanovllm/layers/layernorm.py:16-25), the neox rotary embedding
+// (qwen3.py:110, nanovllm/layers/rotary_embedding.py:6-14,40-50) and the
+// store of k and v into the FP8 cache (nanovllm/layers/attention.py:61-62,
+// store_kvcache_kernel :11-31).  The reference reads the bf16 projection
+// output three times and writes the normalised and rotated q and k back to
+// HBM before the store reads k again; here each head row of the projection
+// output is read once and q leaves as bf16, k and v as FP8 cache bytes.
+//
+// Layout: the projection output is [N, (Hq + 2 Hkv) * 128] bf16 with row
+// stride qkv_stride elements; a 16-lane group owns one 128-dim head row
+// (lane j: dims 8j .. 8j + 7, one 16-byte load), so a wave covers 4 head
+// rows and every access is a whole 16-byte granule of contiguous rows.
+//
+// Arithmetic, with the reference's rounding points:
+//   RMSNorm:  y = bf16(x * rsqrt(mean(x^2) + eps)) in fp32, then
+//             z = bf16(y * w) (a bf16 product with the bf16 weight);
+//   RoPE:     out[i]      = bf16(z[i] cos_i - z[i + 64] sin_i),
+//             out[i + 64] = bf16(z[i + 64] cos_i + z[i] sin_i), i < 64, fp32 math,
+//             cos/sin from the fp32 cos_sin_cache row of the token's position;
+//             lane j (< 8) and lane j + 8 hold the two halves and swap them
+//             with one cross-lane exchange;
+//   store:    k (after RoPE) and v (as projected) rounded to E4M3FN (RNE,
+//             satfinite), written to slot_mapping[token] unless it is -1.
+// The sum of squares is reduced in a different order from the reference
+// and rsqrt is the hardware's, so an output can differ from it by one bf16
+// ulp where the fp32 value sits at a rounding boundary.
+#include "fp8_common.h"
+#include "kernels.h"
+
+namespace nvamd {
+
+namespace {
+
+constexpr int kLanesPerRow = kHeadDim / 8;  // 16
+
+// 8 floats -> 8 bf16 (RNE) in four dwords
+__device__ __forceinline__ u32x4 pack8_bf16(const float (&v)[8]) {
+  return u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
+}
+
+__device__ __forceinline__ void unpack8_bf16(u32x4 w, float (&v)[8]) {
+  const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = bf16_bits_to_f32(d[i] & 0xFFFFu);
+    v[2 * i + 1] = bf16_bits_to_f32(d[i] >> 16);
+  }
+}
+
+// 8 bf16 values (as floats) -> 8 E4M3FN bytes in two dwords
+__device__ __forceinline__ u32x2 to_fp8x8(const float (&v)[8]) {
+  return u32x2{f32x4_to_fp8x4(v[0], v[1], v[2], v[3]), f32x4_to_fp8x4(v[4], v[5], v[6], v[7])};
+}
+
+__device__ __forceinline__ u32x4 shfl_xor_u32x4(u32x4 w, int mask) {
+  return u32x4{(uint32_t)__shfl_xor((int)w.x, mask, 64), (uint32_t)__shfl_xor((int)w.y, mask, 64),
+               (uint32_t)__shfl_xor((int)w.z, mask, 64), (uint32_t)__shfl_xor((int)w.w, mask, 64)};
+}
+
+}  // namespace
+
+__global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(QkNormRopeParams p) {
+  const int rows_per_token = p.Hq + 2 * p.Hkv;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t row = gid / kLanesPerRow;  // head row over all tokens
+  const int j = (int)(gid % kLanesPerRow);
+  // every lane of a 16-lane group stays until the cross-lane exchange: the
+  // groups of a wave are whole, and the grid covers whole rows
+  const bool live = row < p.num_tokens * rows_per_token;
+  const int64_t tok = live ? row / rows_per_token : 0;
+  const int r = live ? (int)(row - tok * rows_per_token) : 0;
+  const int32_t slot = live ? p.slot_mapping[tok] : -1;
+  const bool store = slot >= 0 && (int64_t)slot < p.num_slots;
+  const int64_t cache_row = (int64_t)slot * p.Hkv * kHeadDim;
+
+  float x[8];
+  unpack8_bf16(live ? *reinterpret_cast<const u32x4*>(p.qkv + tok * p.qkv_stride + (int64_t)r * kHeadDim + 8 * j)
+                    : u32x4{0u, 0u, 0u, 0u},
+               x);
+  if (r >= p.Hq + p.Hkv) {  // v: stored as projected
+    if (live && store)
+      *reinterpret_cast<u32x2*>(p.v_cache + cache_row + (int64_t)(r - p.Hq - p.Hkv) * kHeadDim + 8 * j) = to_fp8x8(x);
+    return;  // whole groups take this branch: a row is q, k or v for all its lanes
+  }
+  const bool is_q = r < p.Hq;
+
+  // RMSNorm over the row's 128 dims (the 16 lanes of the group)
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(x[i], x[i], ss);
+#pragma unroll
+  for (int m = 1; m < kLanesPerRow; m <<= 1) ss += shfl_xor_f32(ss, m);
+  const float rs = __builtin_amdgcn_rsqf(ss * (1.0f / kHeadDim) + p.eps);
+  float w[8];
+  unpack8_bf16(*reinterpret_cast<const u32x4*>((is_q ? p.q_weight : p.k_weight) + 8 * j), w);
+  float z[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float y = bf16_bits_to_f32(pack_bf16x2(x[i] * rs, 0.f) & 0xFFFFu);
+    z[i] = bf16_bits_to_f32(pack_bf16x2(y * w[i], 0.f) & 0xFFFFu);
+  }
+
+  // RoPE: lanes j and j ^ 8 hold dims i and i + 64 of the same frequencies
+  const u32x4 zp = pack8_bf16(z);  // exact: z is bf16
+  float other[8];
+  unpack8_bf16(shfl_xor_u32x4(zp, 8), other);
+  int64_t pos = live ? p.positions[tok] : 0;
+  pos = pos < 0 ? 0 : (pos >= p.max_position ? p.max_position - 1 : pos);  // no read outside the table
+  const float* cs = p.cos_sin + pos * kHeadDim + 8 * (j & 7);
+  const f32x4 c0 = *reinterpret_cast<const f32x4*>(cs), c1 = *reinterpret_cast<const f32x4*>(cs + 4);
+  const f32x4 s0 = *reinterpret_cast<const f32x4*>(cs + kHeadDim / 2);
+  const f32x4 s1 = *reinterpret_cast<const f32x4*>(cs + kHeadDim / 2 + 4);
+  const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+  const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+  const float sgn = (j < 8) ? -1.f : 1.f;  // first half: z cos - other sin; second: z cos + other sin
+  float o[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = bf16_bits_to_f32(pack_bf16x2(z[i] * cv[i] + sgn * (other[i] * sv[i]), 0.f) & 0xFFFFu);
+  if (!live) return;
+
+  const u32x4 out = pack8_bf16(o);
+  if (is_q) {
+    *reinterpret_cast<u32x4*>(p.q_out + (tok * p.Hq + r) * kHeadDim + 8 * j) = out;
+    return;
+  }
+  const int hk = r - p.Hq;
+  if (p.k_out != nullptr) *reinterpret_cast<u32x4*>(p.k_out + (tok * p.Hkv + hk) * kHeadDim + 8 * j) = out;
+  if (store) *reinterpret_cast<u32x2*>(p.k_cache + cache_row + (int64_t)hk * kHeadDim + 8 * j) = to_fp8x8(o);
+}
+
+hipError_t launch_qk_norm_rope_store(const QkNormRopeParams& p, hipStream_t stream) {
+  if (p.num_tokens == 0) return hipSuccess;
+  const int64_t threads = p.num_tokens * (p.Hq + 2 * p.Hkv) * kLanesPerRow;
+  const int64_t blocks = (threads + 255) / 256;
+  if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(qk_norm_rope_store_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
+}  // namespace nvamd

@@ -1,0 +1,96 @@
+"""Fused q/k RMSNorm + RoPE + FP8 KV store on the GPU vs the oracle.
+
+q and k are floating point (fp32 math rounded to bf16 at the reference's
+points): within atol/rtol 1e-2 of the oracle, and almost all bit-identical
+(the sum of squares is reduced in another order and rsqrt is the hardware's,
+which can move a value across a bf16 rounding boundary).  The FP8 cache
+bytes are checked byte-exactly: V against the oracle's quantisation of the
+projected v, K against the quantisation of the kernel's own k output."""
+import numpy as np
+import pytest
+import torch
+
+import workloads as W
+from gpu_util import TOL, announce, assert_close
+from oracle import fp8 as ofp8
+from oracle import qk_norm_rope as oq
+from nanovllm_amd.layers.qk_norm_rope import qk_norm_rope_store
+
+pytestmark = pytest.mark.gpu
+D = 128
+
+
+def _case(n, hq, hkv, slots, positions, max_pos, num_blocks, bs=256, seed=0, row_pad=0, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    width = (hq + 2 * hkv) * D
+    base = (torch.randn(n, width + row_pad, generator=g) * scale).to(torch.bfloat16)
+    qkv_cpu = base[:, :width]
+    wq = (1.0 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    wk = (1.0 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    cache = oq.rope_cache(D, max_pos, 1e6)
+    kc_cpu = torch.zeros(num_blocks, bs, hkv, D, dtype=torch.uint8)
+    vc_cpu = torch.zeros_like(kc_cpu)
+    q_want, k_want = oq.qk_norm_rope_store(qkv_cpu, hq, hkv, D, positions, wq, wk, 1e-6, cache, kc_cpu, vc_cpu, slots)
+    base_g = base.cuda()
+    qkv = base_g[:, :width]
+    kc = torch.zeros(num_blocks, bs, hkv, D, dtype=torch.uint8, device="cuda").view(torch.float8_e4m3fn)
+    vc = torch.zeros_like(kc)
+    q, k = qk_norm_rope_store(positions.cuda(), qkv, wq.cuda(), wk.cuda(), 1e-6, cache.cuda().unsqueeze(1), kc, vc,
+                              slots.cuda(), hq, hkv, D, return_k=True)
+    torch.cuda.synchronize()
+    return (q.cpu(), k.cpu(), kc.view(torch.uint8).cpu(), vc.view(torch.uint8).cpu(),
+            q_want, k_want, kc_cpu, vc_cpu, qkv_cpu)
+
+
+def _check(res, hq, hkv, slots, what):
+    q, k, kc, vc, q_want, k_want, kc_want, vc_want, qkv = res
+    assert_close(q, q_want, f"{what}: q")
+    assert_close(k, k_want, f"{what}: k")
+    exact_q = (q.view(torch.int16) == q_want.view(torch.int16)).float().mean().item()
+    exact_k = (k.view(torch.int16) == k_want.view(torch.int16)).float().mean().item()
+    print(f"[qk-norm-rope] {what}: q bit-identical {exact_q:.5f}, k {exact_k:.5f}", flush=True)
+    assert exact_q > 0.99 and exact_k > 0.99
+    n = q.shape[0]
+    v = qkv[:, (hq + hkv) * D:].reshape(n, hkv, D)
+    kf, vf = kc.view(-1, hkv * D), vc.view(-1, hkv * D)
+    kw, vw = kc_want.view(-1, hkv * D), vc_want.view(-1, hkv * D)
+    valid = slots >= 0
+    s = slots[valid].long()
+    assert torch.equal(vf[s], ofp8.quantize_bf16_tensor(v[valid].reshape(-1, hkv * D))), f"{what}: V bytes"
+    assert torch.equal(kf[s], ofp8.quantize_bf16_tensor(k[valid].reshape(-1, hkv * D))), f"{what}: K bytes"
+    untouched = torch.ones(kf.shape[0], dtype=torch.bool)
+    untouched[s] = False
+    assert bool((kf[untouched] == 0).all()) and bool((vf[untouched] == 0).all()), f"{what}: stray cache writes"
+    assert torch.equal(vf, vw)
+    # K bytes equal the oracle's wherever k is bit-identical
+    same_rows = (k.view(torch.int16) == k_want.view(torch.int16)).reshape(n, -1).all(dim=1) & valid
+    assert torch.equal(kf[slots[same_rows].long()], kw[slots[same_rows].long()])
+
+
+def test_qwen3_8b_prefill_tokens():
+    """The prefill workload's 8,192 new tokens at Qwen3-8B shapes (32/8 heads):
+    positions cached .. cached + 511 per sequence, slots from its block tables."""
+    wl = W.qwen3_8b_prefill()
+    announce("qk_norm_rope_store: 8192 tokens, 32/8 heads")
+    slots = torch.from_numpy(wl.new_token_slots())
+    positions = torch.from_numpy(np.concatenate([np.arange(s.cached, s.lk) for s in wl.seqs])).to(torch.int64)
+    res = _case(len(slots), 32, 8, slots, positions, 40960, wl.num_blocks, seed=1)
+    _check(res, 32, 8, slots, "qwen3-8b prefill tokens")
+
+
+@pytest.mark.parametrize("n,hq,hkv", [(1, 32, 8), (3, 4, 1), (37, 24, 8), (100, 64, 8), (9, 16, 2)])
+def test_ragged_shapes_padding_slots_and_strided_rows(n, hq, hkv):
+    """Odd token counts (partial workgroups), several GQA ratios, slot -1 rows
+    (no cache write), positions 0 and the last table row, and a projection
+    output whose rows are longer than q + k + v (row stride > row)."""
+    rng = np.random.default_rng(n * 100 + hq + hkv)
+    nb, bs, max_pos = 8, 16, 4096
+    slots = torch.from_numpy(rng.permutation(nb * bs)[:n].astype(np.int32))
+    slots[::3] = -1
+    positions = torch.from_numpy(rng.integers(0, max_pos, size=n)).to(torch.int64)
+    positions[0] = 0
+    if n > 1:
+        positions[-1] = max_pos - 1
+    announce(f"qk_norm_rope_store: N={n}, {hq}/{hkv} heads")
+    res = _case(n, hq, hkv, slots, positions, max_pos, nb, bs=bs, seed=n, row_pad=64, scale=4.0)
+    _check(res, hq, hkv, slots, f"N={n} {hq}/{hkv}")
