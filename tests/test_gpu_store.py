@@ -78,3 +78,25 @@ def test_store_workload_matches_oracle(make):
     announce(f"store: workload {wl.name}")
     from gpu_util import build_pair
     build_pair(wl)
+
+
+@pytest.mark.parametrize("hkv,d", [(2, 128), (1, 48), (3, 10)])
+def test_store_each_kernel_path(hkv, d):
+    """Rows of a multiple of 32 elements (two-chunk kernel), of 16 (one-chunk
+    kernel) and of neither (one element per lane), with canaries around every
+    written row and a slot of -1."""
+    announce(f"store: row of {hkv}x{d} elements")
+    torch.manual_seed(1)
+    N, P, bs = 29, 3, 16
+    k = (torch.randn(N, hkv, d) * 300).to(torch.bfloat16)
+    v = (torch.randn(N, hkv, d) * 0.01).to(torch.bfloat16)
+    slots = torch.randperm(P * bs)[:N].to(torch.int32)
+    slots[3] = -1
+    kc = torch.full((P, bs, hkv, d), 0x5A, dtype=torch.uint8, device="cuda").view(FP8)
+    vc = torch.full((P, bs, hkv, d), 0xA5, dtype=torch.uint8, device="cuda").view(FP8)
+    store_kvcache(k.cuda(), v.cuda(), kc, vc, slots.cuda())
+    kc_ref = torch.full((P, bs, hkv, d), 0x5A, dtype=torch.uint8)
+    vc_ref = torch.full((P, bs, hkv, d), 0xA5, dtype=torch.uint8)
+    ofp8.store_kvcache(k, v, kc_ref, vc_ref, slots)
+    assert torch.equal(kc.view(torch.uint8).cpu(), kc_ref)
+    assert torch.equal(vc.view(torch.uint8).cpu(), vc_ref)
