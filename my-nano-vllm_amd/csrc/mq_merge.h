@@ -92,9 +92,60 @@ __host__ __device__ __forceinline__ int merge_slices(const MqParams& p, int n_wa
 
 // ---- balanced (stream-K) kernel: merge of a pair cut across workgroups ----
 
-// Workgroup holding stage x of T split over W workgroups.
-__device__ __forceinline__ int sk_owner(int64_t x, int64_t T, int W) {
-  return (int)(((x + 1) * W + T - 1) / T) - 1;
+// Stream-K ranges of the balanced decode kernel.  Workgroup w gets a share
+// of the T stages proportional to its weight: a for even w, kSkPairWeight - a
+// for odd w.  Workgroups are dealt to the 8 XCDs round-robin, so even
+// workgroups run on even-numbered XCDs; on MI355X those stream this kernel's
+// KV bytes 5-10% faster than the odd-numbered ones when every CU is loading
+// at full rate (per-workgroup wall-clock timestamps, on several boxes), and
+// equal shares then leave the even XCDs idle at the end.  Decode runs at
+// that rate and takes a = kSkEvenWeight; the short-query rows of a varlen
+// call do not, and take equal shares.  The split is fixed, so results do
+// not depend on timing.  With C(w) = the weight of workgroups 0 .. w-1,
+// workgroup w owns stages [T C(w) / C(W), T C(w+1) / C(W)).
+constexpr int kSkPairWeight = 64, kSkEvenWeight = 33;
+
+__device__ __forceinline__ int sk_even_weight(const MqParams& p) {
+  return p.cu_q == nullptr ? kSkEvenWeight : kSkPairWeight / 2;
+}
+
+// C(w) in the integer type U (uint32_t when T * C(W) + T < 2^32, see
+// sk_fits32, else uint64_t: a 64-bit division is a long instruction
+// sequence, so each caller picks the type once and does all its range
+// arithmetic in it).
+template <typename U>
+__device__ __forceinline__ U sk_cum_weight(U w, U a) {
+  return (w >> 1) * (U)kSkPairWeight + (w & 1) * a;
+}
+
+__device__ __forceinline__ bool sk_fits32(int64_t T, int W, int a) {
+  return (T * (sk_cum_weight<uint64_t>((uint64_t)W, (uint64_t)a) + 1)) >> 32 == 0;
+}
+
+// First stage of workgroup w's range.
+template <typename U>
+__device__ __forceinline__ U sk_range_start(U w, U T, U W, U a) {
+  return T * sk_cum_weight<U>(w, a) / sk_cum_weight<U>(W, a);
+}
+
+// Workgroup holding stage x (0 <= x < T): the last w with T C(w) / C(W) <= x,
+// i.e. with C(w) <= ceil((x + 1) C(W) / T) - 1.
+template <typename U>
+__device__ __forceinline__ int sk_owner(U x, U T, U W, U a) {
+  const U cmax = ((x + 1) * sk_cum_weight<U>(W, a) + T - 1) / T - 1;
+  const U k = cmax / (U)kSkPairWeight, r = cmax % (U)kSkPairWeight;
+  const U w = 2 * k + (r >= a ? 1 : 0);
+  return (int)(w < W - 1 ? w : W - 1);
+}
+
+// Owners of a pair's first (stage P) and last (P + n - 1) stages, and
+// whether the pair starts after the first owner's range does (then it is
+// that workgroup's last pair: slot 1).
+template <typename U>
+__device__ __forceinline__ void sk_pair_owners(U P, U n, U T, U W, U a, int& wf, int& wl, int& slot_f) {
+  wf = sk_owner<U>(P, T, W, a);
+  wl = sk_owner<U>(P + n - 1, T, W, a);
+  slot_f = sk_range_start<U>((U)wf, T, W, a) < P ? 1 : 0;
 }
 
 // Merges the partials of one (query row, head) whose pair was cut across
@@ -131,17 +182,10 @@ __device__ __forceinline__ void sk_merge_one(const MqParams& p, int b, int idx, 
   // 32-bit arithmetic when T * (W + 1) < 2^32 (every product below is then
   // below 2^32), since a 64-bit division is a long instruction sequence and
   // this pass runs one per wave
+  const int a = sk_even_weight(p);
   int wf, wl, slot_f;
-  if (T < (int64_t)(0xffffffffu / (uint32_t)(W + 1))) {
-    const uint32_t t = (uint32_t)T, uw = (uint32_t)W, p0 = (uint32_t)P;
-    wf = (int)(((p0 + 1u) * uw + t - 1u) / t) - 1;
-    wl = (int)(((p0 + (uint32_t)n) * uw + t - 1u) / t) - 1;
-    slot_f = ((uint32_t)wf * t / uw < p0) ? 1 : 0;
-  } else {
-    wf = sk_owner(P, T, W);
-    wl = sk_owner(P + n - 1, T, W);
-    slot_f = ((int64_t)wf * T / W < P) ? 1 : 0;
-  }
+  if (sk_fits32(T, W, a)) sk_pair_owners<uint32_t>((uint32_t)P, (uint32_t)n, (uint32_t)T, (uint32_t)W, (uint32_t)a, wf, wl, slot_f);
+  else sk_pair_owners<uint64_t>((uint64_t)P, (uint64_t)n, (uint64_t)T, (uint64_t)W, (uint64_t)a, wf, wl, slot_f);
   if (wf == wl) return;  // finished by its workgroup
   // Workgroups in (wf, wl] start inside the pair, so it is their first pair
   // (slot 0); wf holds it in slot 0 if its range starts at P, else in slot 1
@@ -164,7 +208,9 @@ __device__ __forceinline__ void sk_merge_one(const MqParams& p, int b, int idx, 
     if (may_be_empty) {
 #pragma nounroll
       for (int j = 0; j < cnt; ++j)
-        if ((int64_t)(w0 + j) * T / W == (int64_t)(w0 + j + 1) * T / W) skip |= 1u << j;
+        if (sk_range_start<uint32_t>(w0 + j, (uint32_t)T, W, a) ==  // T < W: T * C(W) < 2^32
+            sk_range_start<uint32_t>(w0 + j + 1, (uint32_t)T, W, a))
+          skip |= 1u << j;
     }
     uint32_t a[8];  // dims 2 lane, 2 lane + 1 of contributor j's acc / l (fp16)
 #pragma unroll

@@ -596,7 +596,8 @@ __global__ __launch_bounds__(256) void paged_mq_attn_kernel(MqParams p) {
 template <int NCB, int HG>
 __global__ __launch_bounds__(256) void prefill_short_kernel(MqParams p, PrefillParams pp, PrefillItem* items) {
   if ((int)blockIdx.z == p.num_seqs) {
-    if (blockIdx.x == 0 && blockIdx.y == 0) prefill_schedule(pp, items);
+    __shared__ int sched_lds[kScheduleLdsInts];
+    if (blockIdx.x == 0 && blockIdx.y == 0) prefill_schedule(pp, items, sched_lds);
     return;
   }
   mq_attn<NCB, HG>(p, blockIdx.x, blockIdx.y, blockIdx.z);
@@ -627,10 +628,12 @@ __global__ __launch_bounds__(256) void mq_reduce_varlen_kernel(MqParams p) {
 // (sequence b, group hg of HG kv heads, HG = 8 when Hkv % 8 == 0, else 4);
 // its n_b = ceil(L_b / 16) stages of 16 tokens are laid end to end in
 // (b, hg) order, T stages in all.  Workgroup w of a persistent grid of W
-// (as many as stay resident) streams stages [w*T/W, (w+1)*T/W), so every
-// workgroup moves the same KV bytes whatever the context lengths; the
-// uneven per-sequence workgroups of paged_mq_attn_kernel leave the machine
-// half idle at the end of a batch.  Wave i owns kv head HG*hg + i and all
+// (as many as stay resident) streams a fixed share of about T/W stages
+// (sk_range_start: in decode a little more on the faster even-numbered
+// XCDs), so the work
+// per workgroup does not depend on the context lengths; the uneven
+// per-sequence workgroups of paged_mq_attn_kernel leave the machine half
+// idle at the end of a batch.  Wave i owns kv head HG*hg + i and all
 // 16 tokens of each stage (a 128-byte slice of each token row; with HG = 8
 // a stage row is a whole 1 KiB cache row), so no cross-wave merge is
 // needed.  A pair inside one range is finished by its workgroup; a pair cut
@@ -694,15 +697,16 @@ struct SkStage {
 // prefill kernel's work list (items != nullptr).
 template <int NCB, int HG, bool QL>
 __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p, PrefillParams pp, PrefillItem* items) {
-  if (items != nullptr && (int)blockIdx.x == p.sk_wgs) {
-    prefill_schedule(pp, items);
-    return;
-  }
   using S = SkStage<HG, QL>;
   static_assert(HG == 4 || HG == 8, "4 or 8 kv heads per workgroup");
   static_assert(!QL || NCB == 1, "queries through LDS for G <= 8 only");
   constexpr int kRingBytes = S::kRing;
+  static_assert(kRingBytes >= 4 * kScheduleLdsInts, "the schedule borrows the ring");
   __shared__ __attribute__((aligned(16))) uint8_t smem[kRingBytes];
+  if (items != nullptr && (int)blockIdx.x == p.sk_wgs) {
+    prefill_schedule(pp, items, reinterpret_cast<int*>(smem));
+    return;
+  }
   const uint32_t lds_smem = wave_uniform((int)lds_addr(smem));
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = wave_uniform(tid >> 6);
@@ -744,15 +748,17 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p, PrefillP
   const int64_t T = (int64_t)NHG * carry;
   if (w == 0)
     for (int b = tid; b <= B; b += kThreads) p.sk_prefix[b] = pre[b];
-  // the range [w*T/W, (w+1)*T/W): in 32-bit arithmetic when (W+1)*T < 2^32
-  // (a 64-bit division is a long instruction sequence on the prologue's path)
+  // this workgroup's share of the stages (sk_range_start)
   int64_t start, end;
-  if (T < (int64_t)(0xffffffffu / (uint32_t)(W + 1))) {
-    start = (uint32_t)w * (uint32_t)T / (uint32_t)W;
-    end = (uint32_t)(w + 1) * (uint32_t)T / (uint32_t)W;
-  } else {
-    start = (int64_t)w * T / W;
-    end = (int64_t)(w + 1) * T / W;
+  {
+    const int a = sk_even_weight(p);
+    if (sk_fits32(T, W, a)) {
+      start = sk_range_start<uint32_t>(w, (uint32_t)T, W, a);
+      end = sk_range_start<uint32_t>(w + 1, (uint32_t)T, W, a);
+    } else {
+      start = (int64_t)sk_range_start<uint64_t>(w, T, W, a);
+      end = (int64_t)sk_range_start<uint64_t>(w + 1, T, W, a);
+    }
   }
   if (start >= end) return;
   // first pair: the last sequence b0 with NHG * pre[b0] <= start

@@ -99,12 +99,15 @@ __device__ __forceinline__ int block_incl_scan(int x, int* warp_tot, int& total)
 // are written in decreasing tile count (counting sort), followed by records
 // with seq = -1 up to n_records.  Each thread keeps the geometry of its
 // first kSchedCached candidates in registers, so the passes over the items
-// read the sequence lengths from memory once.
+// read the sequence lengths from memory once.  `lds` is the caller's LDS,
+// at least kScheduleLdsInts ints (the workgroup that runs the schedule uses
+// no other LDS, so the caller lends it its own buffer).
 constexpr int kSchedCached = 4;
+constexpr int kScheduleLdsInts = kCostBuckets + 4;
 
-__device__ __forceinline__ void prefill_schedule(const PrefillParams& p, PrefillItem* __restrict__ items) {
-  __shared__ int hist[kCostBuckets];
-  __shared__ int warp_tot[4];
+__device__ __forceinline__ void prefill_schedule(const PrefillParams& p, PrefillItem* __restrict__ items, int* lds) {
+  int* hist = lds;                    // [kCostBuckets]
+  int* warp_tot = lds + kCostBuckets;  // [4]
   const int tid = threadIdx.x;
   const bool worker = tid < 256;
   const int n_items_max = p.num_seqs * p.n_mblocks;
