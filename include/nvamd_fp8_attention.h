@@ -48,8 +48,8 @@ extern "C" {
 #define NVAMD_ERR_WORKSPACE 3
 #define NVAMD_ERR_LAUNCH 4
 
-/* ABI version of this header (bumped on any signature change). */
-#define NVAMD_ABI_VERSION 4
+/* ABI version of this header and nvamd_fp8_linear.h (bumped on any signature change). */
+#define NVAMD_ABI_VERSION 5
 int32_t nvamd_abi_version(void);
 
 /* Description of the last error on the calling thread ("" if none). */

@@ -1,5 +1,6 @@
-// C ABI entry points (declared in include/nvamd_fp8_attention.h): argument
-// validation, static partition sizing and kernel launches.
+// C ABI entry points (declared in include/nvamd_fp8_attention.h and
+// include/nvamd_fp8_linear.h): argument validation, static partition sizing
+// and kernel launches.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -11,6 +12,7 @@
 
 #include "kernels.h"
 #include "nvamd_fp8_attention.h"
+#include "nvamd_fp8_linear.h"
 
 // Scratch of nvamd_fp8_decode_attention_noalloc: device memory the library
 // holds for the whole process on every GPU it runs on (each GPU has its own
@@ -269,6 +271,68 @@ int32_t nvamd_qk_norm_rope_store(const void* qkv, int64_t qkv_stride0, const int
   p.Hkv = num_kv_heads;
   p.eps = eps;
   return launch_status(nvamd::launch_qk_norm_rope_store(p, (hipStream_t)stream), fn);
+}
+
+int32_t nvamd_fp8_act_quant(const void* x, int64_t x_stride0, int32_t x_dtype, void* xq, void* x_scale, int64_t M,
+                            int64_t K, void* stream) {
+  static const char* fn = "fp8_act_quant";
+  if (M < 0 || K <= 0 || K % 128 != 0 || x_stride0 < K)
+    return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: bad sizes (M=%lld K=%lld stride=%lld; K %% 128 == 0)", fn,
+                (long long)M, (long long)K, (long long)x_stride0);
+  if (x_dtype != NVAMD_DTYPE_BF16 && x_dtype != NVAMD_DTYPE_F16)
+    return fail(NVAMD_ERR_UNSUPPORTED, "%s: x_dtype must be bf16 or fp16 (got %d)", fn, x_dtype);
+  if (M == 0) return ok();
+  if (!x || !xq || !x_scale) return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+  if ((uintptr_t)x % 16 != 0 || x_stride0 % 8 != 0 || (uintptr_t)xq % 8 != 0 || (uintptr_t)x_scale % 2 != 0)
+    return fail(NVAMD_ERR_UNSUPPORTED, "%s: x must be 16-byte aligned with a row stride of 8 elements (xq 8-byte aligned)",
+                fn);
+  return launch_status(nvamd::launch_fp8_act_quant(x, x_stride0, x_dtype == NVAMD_DTYPE_F16, xq, x_scale, M, K,
+                                                   (hipStream_t)stream),
+                       fn);
+}
+
+int32_t nvamd_fp8_block_gemm(const void* xq, const void* x_scale, const void* weight, int64_t weight_stride0,
+                             const void* weight_scale, void* out, int64_t out_stride0, int32_t out_dtype, int64_t M,
+                             int64_t N, int64_t K, void* stream) {
+  static const char* fn = "fp8_block_gemm";
+  if (M < 0 || N <= 0 || K <= 0 || N % 128 != 0 || K % 128 != 0 || weight_stride0 < K || out_stride0 < N ||
+      N > 0x7fffffffll || K > 0x7fffffffll)
+    return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: bad sizes (M=%lld N=%lld K=%lld; N, K multiples of 128)", fn,
+                (long long)M, (long long)N, (long long)K);
+  if (out_dtype != NVAMD_DTYPE_BF16 && out_dtype != NVAMD_DTYPE_F16)
+    return fail(NVAMD_ERR_UNSUPPORTED, "%s: out_dtype must be bf16 or fp16 (got %d)", fn, out_dtype);
+  if (M == 0) return ok();
+  if (!xq || !x_scale || !weight || !weight_scale || !out) return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+  if ((uintptr_t)xq % 16 != 0 || (uintptr_t)x_scale % 16 != 0 || (uintptr_t)weight % 16 != 0 ||
+      weight_stride0 % 16 != 0 || (uintptr_t)weight_scale % 16 != 0 || (uintptr_t)out % 8 != 0 || out_stride0 % 4 != 0)
+    return fail(NVAMD_ERR_UNSUPPORTED,
+                "%s: operands must be 16-byte aligned (out 8), weight row stride a multiple of 16 bytes, out row stride "
+                "a multiple of 4 elements",
+                fn);
+  if (weight_stride0 * 256 > 0xffffffffll || M * K > (1ll << 46))
+    return fail(NVAMD_ERR_UNSUPPORTED, "%s: weight row stride or activation size beyond 32-bit tile offsets", fn);
+  int dev = 0, lds_limit = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&lds_limit, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || lds_limit <= 0)
+    lds_limit = 160 * 1024;
+  const int Kc = (int)(K / 128);
+  const int config = nvamd::fp8_gemm_pick_config(M, N, Kc, device_cu_count(), lds_limit);
+  if (config < 0)
+    return fail(NVAMD_ERR_UNSUPPORTED, "%s: K=%lld needs more LDS for the tile scales than the device has", fn,
+                (long long)K);
+  nvamd::Fp8GemmParams p{};
+  p.xq = static_cast<const uint8_t*>(xq);
+  p.x_scale = static_cast<const uint16_t*>(x_scale);
+  p.w = static_cast<const uint8_t*>(weight);
+  p.w_scale = static_cast<const uint16_t*>(weight_scale);
+  p.out = static_cast<uint16_t*>(out);
+  p.w_stride = weight_stride0;
+  p.out_stride = out_stride0;
+  p.M = M;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.Kc = Kc;
+  return launch_status(nvamd::launch_fp8_block_gemm(p, config, out_dtype == NVAMD_DTYPE_F16, (hipStream_t)stream), fn);
 }
 
 int64_t nvamd_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t num_kv_heads,

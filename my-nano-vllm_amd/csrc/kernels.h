@@ -106,6 +106,25 @@ struct QkNormRopeParams {
 
 hipError_t launch_qk_norm_rope_store(const QkNormRopeParams& p, hipStream_t stream);
 
+// FP8 block-scaled linear (128 x 128 weight blocks, 128-wide activation groups).
+struct Fp8GemmParams {
+  const uint8_t* xq;        // E4M3FN [M, K], row stride K
+  const uint16_t* x_scale;  // bf16 [M, K / 128]
+  const uint8_t* w;         // E4M3FN [N, K], row stride w_stride (bytes)
+  const uint16_t* w_scale;  // bf16 [N / 128, K / 128]
+  uint16_t* out;            // bf16 or fp16 [M, N], row stride out_stride (elements)
+  int64_t w_stride, out_stride;
+  int64_t M;
+  int N, K, Kc;
+};
+
+hipError_t launch_fp8_act_quant(const void* x, int64_t x_stride, bool f16_in, void* xq, void* x_scale, int64_t M,
+                                int64_t K, hipStream_t stream);
+// Tile configuration for an M x N x K GEMM on `cus` CUs (-1: none fits lds_limit).
+int fp8_gemm_pick_config(int64_t M, int64_t N, int Kc, int cus, int64_t lds_limit);
+int64_t fp8_gemm_lds_bytes(int config, int Kc);
+hipError_t launch_fp8_block_gemm(const Fp8GemmParams& p, int config, bool f16_out, hipStream_t stream);
+
 hipError_t launch_kv_store(const void* key, int64_t key_stride, const void* value,
                            int64_t value_stride, void* k_cache, void* v_cache,
                            const int32_t* slot_mapping, int64_t num_tokens, int row_elems,

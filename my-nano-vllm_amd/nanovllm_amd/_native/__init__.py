@@ -16,14 +16,14 @@ import torch  # noqa: F401  (loads torch's HIP runtime first)
 
 LIB_NAME = "libnvamd_fp8attn.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _c_void_p = ctypes.c_void_p
 _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64
 _f32 = ctypes.c_float
 
-# name -> (restype, argtypes); mirrors include/nvamd_fp8_attention.h
+# name -> (restype, argtypes); mirrors include/nvamd_fp8_attention.h and include/nvamd_fp8_linear.h
 SIGNATURES = {
     "nvamd_abi_version": (_i32, []),
     "nvamd_last_error": (ctypes.c_char_p, []),
@@ -39,6 +39,9 @@ SIGNATURES = {
     "nvamd_fp8_decode_attention_noalloc": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                                   _c_void_p, _i32, _i32, _i32, _i32, _i64, _i32, _i32,
                                                   _f32, _c_void_p]),
+    "nvamd_fp8_act_quant": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _i64, _i64, _c_void_p]),
+    "nvamd_fp8_block_gemm": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i32,
+                                    _i64, _i64, _i64, _c_void_p]),
     "nvamd_prefill_workspace_bytes": (_i64, [_i64, _i32, _i32, _i32, _i64, _i32, _i32, _i32]),
     "nvamd_fp8_prefill_attention": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                            _c_void_p, _c_void_p, _i64, _i32, _i32, _i32, _i32,

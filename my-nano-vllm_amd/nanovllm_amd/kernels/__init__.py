@@ -1,1 +1,1 @@
-"""FP8 attention kernels (gfx950)."""
+"""FP8 attention and FP8 block-scaled linear kernels (gfx950)."""

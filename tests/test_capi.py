@@ -9,11 +9,11 @@ import pytest
 from nanovllm_amd import _native
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "nvamd_fp8_attention.h")
+INCLUDE = os.path.join(ROOT, "include")
 
 
 def _declared():
-    text = open(HEADER).read()
+    text = "".join(open(os.path.join(INCLUDE, f)).read() for f in sorted(os.listdir(INCLUDE)) if f.endswith(".h"))
     return sorted(set(re.findall(r"\b(nvamd_[a-z0-9_]+)\s*\(", text)))
 
 
@@ -67,3 +67,16 @@ def test_rejects_partition_wider_than_the_block_table_window():
     # the automatic choice never exceeds the window
     nb = lib.nvamd_decode_workspace_bytes(1, 8, 2, 4096, 256, 0)
     assert nb > 0  # 1M-token capacity must be split
+
+
+def test_fp8_linear_rejects_bad_shapes_without_gpu():
+    """K and N must be multiples of the 128 block (fp8_linear.py:114)."""
+    lib = _native.load()
+    assert lib.nvamd_fp8_act_quant(None, 100, 0, None, None, 4, 100, None) == 1
+    assert b"K % 128" in lib.nvamd_last_error()
+    assert lib.nvamd_fp8_act_quant(None, 128, 2, None, None, 4, 128, None) == 2
+    assert lib.nvamd_fp8_act_quant(None, 128, 0, None, None, 4, 128, None) == 1
+    assert b"null pointer" in lib.nvamd_last_error()
+    assert lib.nvamd_fp8_block_gemm(None, None, None, 256, None, None, 200, 0, 4, 200, 256, None) == 1
+    assert lib.nvamd_fp8_block_gemm(None, None, None, 256, None, None, 256, 3, 4, 256, 256, None) == 2
+    assert lib.nvamd_fp8_block_gemm(None, None, None, 256, None, None, 256, 0, 0, 256, 256, None) == 0

@@ -127,9 +127,10 @@ def test_prefill_lq1_equals_decode():
     """Lq = 1 prefill rows against decode: at this shape (Hkv % 4 == 0, paged)
     both run the balanced stream-K kernel over the same stages.  Decode gives
     the even-numbered workgroups a slightly larger share than a varlen call
-    does, so the two cut pairs at different stages and may differ by the
-    rounding of the merge (one bf16 ulp); each stays within the tolerance of
-    the oracle."""
+    does, so the two cut pairs at different stages and differ by the rounding
+    of the merge: one bf16 ulp, or 2^-10 absolute where a cut pair's fp16
+    partial (2^-11 of the V values) meets cancellation; each stays within the
+    tolerance of the oracle."""
     announce("prefill: Lq=1 rows equal decode")
     wl = W.qwen3_0p6b_decode(B=24)
     cpu_c, gpu_c = build_pair(wl)
@@ -141,7 +142,7 @@ def test_prefill_lq1_equals_decode():
                                torch.from_numpy(wl.context_lens()), SCALE)
     assert_close(dec, want, "decode")
     assert_close(pre, want, "Lq=1 prefill")
-    torch.testing.assert_close(pre.float(), dec.float(), rtol=2.0 ** -7, atol=1e-6,
+    torch.testing.assert_close(pre.float(), dec.float(), rtol=2.0 ** -7, atol=2.0 ** -10,
                                msg="Lq=1 prefill vs decode: more than one bf16 ulp apart")
 
 
