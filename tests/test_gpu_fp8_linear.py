@@ -12,9 +12,11 @@ below the block's largest product is dropped: measured with cancelling
 FP8 dot product NVIDIA's tensor cores compute for the reference, which is why
 the reference promotes to fp32 every 128 elements.  On random codes the
 largest error seen is 2^-15 of the sum of absolute terms; a misplaced or
-missing K block errs by about 2^-3.5 of it.  Shapes are chosen so that on a 256-CU MI355X the library
-picks each of its four tile shapes (256x128, 128x64, 128x32, 64x16 features x
-tokens): it takes the largest tile whose grid still covers the CUs.
+missing K block errs by about 2^-3.5 of it.
+
+Shapes are chosen so that on a 256-CU MI355X the library picks each of its
+tile shapes (128x64, 128x32, 64x16 features x tokens): it takes the largest
+tile whose grid still covers the CUs.
 """
 import numpy as np
 import pytest
@@ -130,7 +132,7 @@ def test_act_quant_unit_scale_all_patterns_and_strided_rows():
     assert np.array_equal(_bits(xs), xs_ref)
 
 
-# (M, N, K): tile chosen on 256 CUs -> 256x128: (2048, 4096, 256); 128x64: (1024, 2048, 256);
+# (M, N, K): tile chosen on 256 CUs -> 128x64: (2048, 4096, 256), (1024, 2048, 256);
 # 128x32: (1024, 1024, 128); 64x16: the small shapes
 TILE_SHAPES = [(2048, 4096, 256), (1024, 2048, 256), (1024, 1024, 128), (24, 256, 512), (1, 128, 128)]
 
