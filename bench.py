@@ -32,7 +32,20 @@ Secondary fields in the same JSON line:
   contiguous_prefill  the mixed batch's 1024-token contiguous-layout prompt
                (block_tables=None), TFLOP/s;
   contiguous_prefill_batch  the prefill workload in the contiguous layout
-               (its K/V rows gathered per sequence), TFLOP/s.
+               (its K/V rows gathered per sequence), TFLOP/s;
+  fp8_linear   the FP8 block-scaled linear layer at Qwen3-8B shapes: the qkv
+               projection of the 16 x 512-token prefill step (M = 8192, N =
+               6144, K = 4096) in TFLOP/s vs the dense FP8 MFMA peak, and the
+               gate/up projection of the 192 decode rows (M = 192, N = 24576)
+               in GB/s of weights vs HBM; the activation quantisation and the
+               whole fp8_block_linear call beside each, and an oracle CPU
+               baseline;
+  metadata     one engine step's attention metadata (positions, slots,
+               cu_seqlens, context lengths, block tables) for the mixed batch
+               and for the 16 x 512 prefill step: host time per call and time
+               to completion of the on-device build and of the vectorised host
+               build, the on-device build's GPU time, and, as CPU baseline,
+               the reference's own per-token loops and per-tensor copies.
 These are timed after 0.15 s of sustained warm-up calls (the shader clock
 settles lower under continuous MFMA load within the first tens of
 milliseconds); the headline decode field runs exactly --warmup warm-up calls.
@@ -54,7 +67,8 @@ parity tests' checker) on the host cores for a bounded sample of the same
 workload; the prefill field carries one of its own.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--only decode|decode06|prefill|long|store|mixed|all] [--no-cpu-baseline]
+                    [--only decode|decode06|prefill|long|store|mixed|linear|metadata|all]
+                    [--no-cpu-baseline]
                     [--copy-probe]
 """
 import argparse
@@ -93,7 +107,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="all", choices=["decode", "decode06", "prefill", "long", "store", "mixed", "all"])
+    ap.add_argument("--only", default="all",
+                    choices=["decode", "decode06", "prefill", "long", "store", "mixed", "linear", "metadata", "all"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 1 GiB device copy (counter scale for rocprofv3 --pmc)")
@@ -270,6 +285,172 @@ def bench_contiguous_batch(wl, pools, q, steps, warmup):
     ms = timed(step, steps, warmup, SECONDARY_WARM_S)
     flops = wl.attention_flops()
     return dict(ms=ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12)
+
+
+FP8_PEAK_TFLOPS = 5000.0       # MI355X dense FP8 MFMA
+
+
+def bench_fp8_linear(M, N, K, steps, warmup, n_weights=2):
+    """The FP8 block-scaled linear layer at one shape: the GEMM alone (on
+    already-quantised activations, the reference's second kernel), the
+    activation quantisation alone, and fp8_block_linear end to end.  Random
+    finite E4M3FN weights; n_weights copies are cycled so that the decode-size
+    GEMM streams its weights from HBM."""
+    from nanovllm_amd import _native
+    from nanovllm_amd.kernels.fp8_linear import fp8_block_linear
+    lib = _native.load()
+    g = torch.Generator(device="cuda").manual_seed(M + N + K)
+    x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    ws = []
+    for _ in range(n_weights):
+        c = torch.randint(0, 256, (N, K), device="cuda", generator=g, dtype=torch.int32).to(torch.uint8)
+        ws.append(torch.where((c & 0x7F) == 0x7F, c ^ 1, c).view(torch.float8_e4m3fn))
+    w_scale = (torch.rand(N // 128, K // 128, device="cuda", generator=g) * 1e-3).to(torch.bfloat16)
+    xq = torch.empty(M, K, dtype=torch.uint8, device="cuda")
+    xs = torch.empty(M, K // 128, dtype=torch.bfloat16, device="cuda")
+    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    _native.check(lib.nvamd_fp8_act_quant(x.data_ptr(), K, 0, xq.data_ptr(), xs.data_ptr(), M, K, stream), "quant")
+
+    def gemm(i):
+        w = ws[i % n_weights]
+        _native.check(lib.nvamd_fp8_block_gemm(xq.data_ptr(), xs.data_ptr(), w.data_ptr(), K, w_scale.data_ptr(),
+                                               out.data_ptr(), N, 0, M, N, K, stream), "gemm")
+
+    def quant(i):
+        _native.check(lib.nvamd_fp8_act_quant(x.data_ptr(), K, 0, xq.data_ptr(), xs.data_ptr(), M, K, stream), "quant")
+
+    ms_gemm = timed(gemm, steps, warmup, warm_s=SECONDARY_WARM_S)
+    ms_quant = timed(quant, steps, warmup)
+    ms_linear = timed(lambda i: fp8_block_linear(x, ws[i % n_weights], w_scale), steps, warmup)
+    flops = 2.0 * M * N * K
+    weight_bytes = N * K + (N // 128) * (K // 128) * 2
+    return dict(ms=ms_gemm, tflops=flops / (ms_gemm * 1e-3) / 1e12,
+                weight_gbs=weight_bytes / (ms_gemm * 1e-3) / 1e9,
+                quant_us=ms_quant * 1e3, quant_gbs=3.0 * M * K / (ms_quant * 1e-3) / 1e9,
+                linear_us=ms_linear * 1e3, flops=flops, weight_bytes=weight_bytes)
+
+
+def cpu_baseline_fp8_linear(N, K, rows=16, target_s=8.0):
+    """The oracle's quantisation + block GEMM (numpy, float64 partials) on a
+    bounded sample: `rows` tokens of the shape, repeated for ~target_s."""
+    from oracle import fp8_linear as ol
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(rows, K, generator=g).to(torch.bfloat16)
+    w = torch.randint(0, 120, (N, K), generator=g, dtype=torch.int32).to(torch.uint8).numpy()
+    w_scale = (torch.rand(N // 128, K // 128, generator=g) * 1e-3).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < target_s or n == 0:
+        ol.block_linear(x, w, w_scale)
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    return dict(value=round(2.0 * rows * N * K / dt / 1e9, 3), unit="GFLOP/s", cores=_blas_threads(), kind="port",
+                sample=f"oracle act_quant + block_gemm on {rows} tokens of the {N}x{K} weight, {n} runs")
+
+
+def _blas_threads():
+    """Threads of the BLAS numpy's matmul runs on (the oracle's GEMM)."""
+    try:
+        from threadpoolctl import threadpool_info
+        n = [p["num_threads"] for p in threadpool_info() if p.get("user_api") == "blas"]
+        if n:
+            return max(n)
+    except Exception:  # noqa: BLE001
+        pass
+    return os.cpu_count() or 1
+
+
+class _StepSeq:
+    """The fields of nano-vLLM's Sequence that the attention metadata reads."""
+    __slots__ = ("num_tokens", "num_cached_tokens", "num_scheduled_tokens", "block_table", "block_size")
+
+    def __init__(self, num_tokens, num_cached_tokens, num_scheduled_tokens, block_table, block_size):
+        self.num_tokens, self.num_cached_tokens = num_tokens, num_cached_tokens
+        self.num_scheduled_tokens, self.block_table, self.block_size = num_scheduled_tokens, block_table, block_size
+
+    @property
+    def num_blocks(self):  # nanovllm/engine/sequence.py:58-60
+        return (self.num_tokens + self.block_size - 1) // self.block_size
+
+    @property
+    def last_block_num_tokens(self):  # nanovllm/engine/sequence.py:62-64
+        return self.num_tokens - (self.num_blocks - 1) * self.block_size
+
+
+def step_sequences(wl):
+    """A workload as one engine step: sequence i has its cached keys plus lq
+    scheduled tokens (plain decode: lq = 1, num_tokens = cached + 1;
+    speculative: 1 + drafts scheduled on num_tokens = cached + 1; prefill
+    chunk: num_tokens = cached + lq), and the block-table prefix covering them."""
+    dseqs, pseqs = [], []
+    bs = wl.block_size
+    for i, sp in enumerate(wl.seqs):
+        table = [int(b) for b in wl.block_tables[i, :-(-sp.lk // bs)]]
+        is_decode = sp.lq == 1 or i < wl.extra.get("split_pt", 0) + wl.extra.get("num_spec_seqs", 0)
+        n_tok = sp.cached + 1 if is_decode else sp.cached + sp.lq
+        (dseqs if is_decode else pseqs).append(_StepSeq(n_tok, sp.cached, sp.lq, table, bs))
+    return dseqs, pseqs
+
+
+def bench_metadata(wl, steps=200, warmup=20):
+    """Per-step metadata build for a workload step: host time of the call and
+    time to completion (call + synchronize), for the on-device build and the
+    vectorised host build, and the GPU time of the on-device build's upload +
+    kernel (HIP events on the current stream)."""
+    from nanovllm_amd.engine import metadata as nm
+    dseqs, pseqs = step_sequences(wl)
+    bs = wl.block_size
+    res = {}
+    for name, fn in (("device", lambda: nm.prepare_sequence_device(dseqs, pseqs, bs)),
+                     ("host_numpy", lambda: nm.prepare_sequence(dseqs, pseqs, bs))):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        host = (time.perf_counter() - t0) / steps
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+            torch.cuda.synchronize()
+        e2e = (time.perf_counter() - t0) / steps
+        res[name] = dict(host_us=round(host * 1e6, 2), to_completion_us=round(e2e * 1e6, 2))
+    step = nm.pack_step(dseqs, pseqs, bs)
+    ms = timed(lambda i: nm.build_device_metadata(step, bs), steps, warmup)
+    res["device"]["gpu_us"] = round(ms * 1e3, 2)
+    res["tokens"], res["sequences"] = step.num_tokens, step.num_seqs
+    return res, dseqs, pseqs
+
+
+def cpu_baseline_metadata(dseqs, pseqs, bs, steps=50):
+    """The reference's own per-step work, restated by the oracle's Python loops
+    (model_runner.py:133-220), plus its per-tensor pinned copies."""
+    from oracle import metadata as om
+    dev = torch.device("cuda")
+
+    def ref_step():
+        m = om.prepare_sequence(dseqs, pseqs, bs)
+        out = [torch.tensor(m["positions"], dtype=torch.int64, pin_memory=True).to(dev, non_blocking=True),
+               torch.tensor(m["slot_mapping"], dtype=torch.int32, pin_memory=True).to(dev, non_blocking=True)]
+        for key in ("context_lens", "cu_seqlens_q", "cu_seqlens_k"):
+            if m[key] is not None:
+                out.append(torch.tensor(m[key], dtype=torch.int32, pin_memory=True).to(dev, non_blocking=True))
+        if m["block_tables"] is not None:
+            out.append(torch.tensor(m["block_tables"], dtype=torch.int32, pin_memory=True).to(dev, non_blocking=True))
+        return out
+
+    for _ in range(5):
+        ref_step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        ref_step()
+    host = (time.perf_counter() - t0) / steps
+    torch.cuda.synchronize()
+    return dict(value=round(host * 1e6, 2), unit="us per step (host)", cores=1, kind="port",
+                sample=f"{steps} steps of the same workload step")
 
 
 def copy_probe(reps=4):
@@ -499,11 +680,50 @@ def main():
         del pools
         torch.cuda.empty_cache()
 
+    if args.only in ("linear", "all"):
+        # Qwen3-8B FP8 checkpoints: the qkv projection of a 16 x 512-token
+        # prefill step (MFMA-bound) and the gate/up projection of the mixed
+        # batch's 192 decode rows (weight-streaming, HBM-bound)
+        big = bench_fp8_linear(8192, 6144, 4096, max(args.steps // 2, 10), max(args.warmup // 2, 3))
+        small = bench_fp8_linear(192, 24576, 4096, max(args.steps, 20), max(args.warmup, 5))
+        log(f"fp8 linear: qkv M=8192 {big['ms'] * 1e3:.1f} us ({big['tflops']:.0f} TFLOP/s); "
+            f"gate_up M=192 {small['ms'] * 1e3:.1f} us ({small['weight_gbs']:.0f} GB/s of weights)")
+        extra["fp8_linear"] = dict(
+            workload="FP8 block-scaled linear (128x128 weight blocks), Qwen3-8B shapes",
+            kernels="block_gemm_kernel (act_quant_kernel timed separately)",
+            prefill_qkv=dict(shape="M=8192 tokens, N=6144, K=4096", ms_per_step=round(big["ms"], 5),
+                             tflops=round(big["tflops"], 1), frac_fp8_peak=round(big["tflops"] / FP8_PEAK_TFLOPS, 4),
+                             algorithmic_flops=big["flops"], quant_us=round(big["quant_us"], 2),
+                             quant_gbs=round(big["quant_gbs"], 1), fp8_block_linear_us=round(big["linear_us"], 2)),
+            decode_gate_up=dict(shape="M=192 tokens, N=24576, K=4096", ms_per_step=round(small["ms"], 5),
+                                weight_gbs=round(small["weight_gbs"], 1),
+                                frac_hbm_peak=round(small["weight_gbs"] / HBM_PEAK_GBS, 4),
+                                algorithmic_bytes=small["weight_bytes"], tflops=round(small["tflops"], 1),
+                                quant_us=round(small["quant_us"], 2),
+                                fp8_block_linear_us=round(small["linear_us"], 2)))
+        if not args.no_cpu_baseline:
+            log("cpu baseline (oracle) for the FP8 linear")
+            extra["fp8_linear"]["cpu_baseline"] = cpu_baseline_fp8_linear(6144, 4096)
+        torch.cuda.empty_cache()
+
+    if args.only in ("metadata", "all"):
+        out = {}
+        for wl in (W.qwen3_8b_mixed(), W.qwen3_8b_prefill()):
+            res, dseqs, pseqs = bench_metadata(wl)
+            if not args.no_cpu_baseline:
+                res["cpu_baseline"] = cpu_baseline_metadata(dseqs, pseqs, wl.block_size)
+            out[wl.name] = res
+            log(f"metadata {wl.name}: device {res['device']['host_us']:.1f} us host / "
+                f"{res['device']['to_completion_us']:.1f} us to completion; host numpy "
+                f"{res['host_numpy']['host_us']:.1f} / {res['host_numpy']['to_completion_us']:.1f} us")
+        extra["metadata"] = dict(workload="one engine step's attention metadata (mixed batch; 16 x 512 prefill)",
+                                 kernels="build_metadata_kernel", **out)
+
     if "value" not in line:   # partial runs (profiling) still print one line
         first = next(iter(extra.values()))
         line.update(metric=METRIC + " (partial run: " + first["workload"] + ")",
                     value=first.get("tflops", first.get("gbs")),
-                    unit="TFLOP/s" if "tflops" in first else "GB/s", ms_per_step=first["ms_per_step"],
+                    unit="TFLOP/s" if "tflops" in first else "GB/s", ms_per_step=first.get("ms_per_step"),
                     config=dict(workload=first["workload"]))
     line.update(n_gpus=1, steps=args.steps, warmup=args.warmup, higher_is_better=True, scaling="weak",
                 vs_baseline=None, dtype="bf16",

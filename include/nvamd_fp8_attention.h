@@ -13,6 +13,8 @@
  *                                   (wrapper fp8_prefill_attention,        nanovllm/kernels/fp8_attention.py:314-353)
  *   nvamd_qk_norm_rope_store     <- q_norm, k_norm, rotary_emb, store_kvcache  nanovllm/models/qwen3.py:107-110,
  *                                   nanovllm/layers/attention.py:61-62
+ *   nvamd_build_attention_metadata <- ModelRunner.prepare_block_tables / prepare_prefill / prepare_decode /
+ *                                   prepare_sequence               nanovllm/engine/model_runner.py:133-220
  *
  * Conventions
  *   - All pointers are device pointers (HIP), except where noted.  No call
@@ -101,6 +103,40 @@ int32_t nvamd_qk_norm_rope_store(const void* qkv, int64_t qkv_stride0, const int
                                  void* k_cache, void* v_cache, const int32_t* slot_mapping, int64_t num_tokens,
                                  int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int64_t num_slots,
                                  void* stream);
+
+/*
+ * One engine step's attention metadata, built on the GPU.  Replaces the
+ * host loops and per-tensor copies of ModelRunner.prepare_sequence
+ * (nanovllm/engine/model_runner.py:203-220 with prepare_decode :188-201,
+ * prepare_prefill :144-186 and prepare_block_tables :133-142).
+ *
+ * packed (device, 16-byte aligned, packed_ints int32 entries): num_seqs
+ *   descriptors {num_tokens, num_cached_tokens, num_scheduled_tokens,
+ *   table_len} in the reference's row order -- the num_plain plain decode
+ *   sequences (num_scheduled_tokens == 1) first, then speculative ones, then
+ *   prefill chunks -- followed by the sequences' block tables back to back.
+ * Outputs, in that order of sequences:
+ *   positions int64 [num_tokens]: len - 1 for plain decode rows, num_cached
+ *     .. num_cached + num_scheduled - 1 for varlen rows;
+ *   slot_mapping int32 [num_slots]: block_table[-1] * block_size +
+ *     last_block_num_tokens - 1 for plain decode rows, block_table[p /
+ *     block_size] * block_size + p % block_size for each varlen position p
+ *     (none for a sequence with an empty table, as in the reference's warm-up);
+ *   context_lens int32 [num_plain];
+ *   cu_seqlens_q / cu_seqlens_k int32 [num_seqs - num_plain + 1] (prefix sums
+ *     of num_scheduled and of num_cached + num_scheduled);
+ *   block_tables int32 [num_table_rows, max_table_len]: the non-empty
+ *     tables, padded with -1.
+ * num_tokens, num_slots and num_table_rows are the output sizes the
+ * descriptors imply (the caller computes them to allocate the outputs);
+ * writes beyond them are dropped.  num_seqs <= 2048.
+ */
+int32_t nvamd_build_attention_metadata(const int32_t* packed, int64_t packed_ints, int32_t num_seqs,
+                                       int32_t num_plain, int32_t block_size, int64_t num_tokens,
+                                       int64_t num_slots, int32_t num_table_rows, int32_t max_table_len,
+                                       int64_t* positions, int32_t* slot_mapping, int32_t* context_lens,
+                                       int32_t* cu_seqlens_q, int32_t* cu_seqlens_k, int32_t* block_tables,
+                                       void* stream);
 
 /* Workspace needed by nvamd_fp8_decode_attention for these static shapes
  * (part_tokens = 0 selects the library's partition size). */

@@ -335,6 +335,50 @@ int32_t nvamd_fp8_block_gemm(const void* xq, const void* x_scale, const void* we
   return launch_status(nvamd::launch_fp8_block_gemm(p, config, out_dtype == NVAMD_DTYPE_F16, (hipStream_t)stream), fn);
 }
 
+int32_t nvamd_build_attention_metadata(const int32_t* packed, int64_t packed_ints, int32_t num_seqs, int32_t num_plain,
+                                       int32_t block_size,
+                                       int64_t num_tokens, int64_t num_slots, int32_t num_table_rows,
+                                       int32_t max_table_len, int64_t* positions, int32_t* slot_mapping,
+                                       int32_t* context_lens, int32_t* cu_seqlens_q, int32_t* cu_seqlens_k,
+                                       int32_t* block_tables, void* stream) {
+  static const char* fn = "build_attention_metadata";
+  if (num_seqs < 0 || num_seqs > nvamd::kMetaMaxSeqs || num_plain < 0 || num_plain > num_seqs || block_size <= 0 ||
+      num_tokens < 0 || num_slots < 0 || num_table_rows < 0 || num_table_rows > num_seqs || max_table_len < 0)
+    return fail(NVAMD_ERR_INVALID_ARGUMENT,
+                "%s: bad sizes (seqs=%d of at most %d, plain=%d, block_size=%d, tokens=%lld, slots=%lld, rows=%d, "
+                "width=%d)",
+                fn, num_seqs, nvamd::kMetaMaxSeqs, num_plain, block_size, (long long)num_tokens, (long long)num_slots,
+                num_table_rows, max_table_len);
+  if (num_seqs == 0) return ok();
+  if (packed_ints < 4ll * num_seqs)
+    return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: packed holds %lld ints, fewer than the %d descriptors", fn,
+                (long long)packed_ints, num_seqs);
+  const int n_var = num_seqs - num_plain;
+  if (!packed || (num_tokens > 0 && !positions) || (num_slots > 0 && !slot_mapping) ||
+      (num_plain > 0 && !context_lens) || (n_var > 0 && (!cu_seqlens_q || !cu_seqlens_k)) ||
+      ((int64_t)num_table_rows * max_table_len > 0 && !block_tables))
+    return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+  if ((uintptr_t)packed % 16 != 0) return fail(NVAMD_ERR_UNSUPPORTED, "%s: packed must be 16-byte aligned", fn);
+  nvamd::AttnMetaParams p{};
+  p.packed = packed;
+  p.packed_ints = packed_ints;
+  p.num_seqs = num_seqs;
+  p.num_plain = num_plain;
+  p.block_size = block_size;
+  p.max_table_len = max_table_len;
+  p.cap_tokens = num_tokens;
+  p.cap_slots = num_slots;
+  p.cap_rows = num_table_rows;
+  p.positions = positions;
+  p.slot_mapping = slot_mapping;
+  p.context_lens = context_lens;
+  p.cu_seqlens_q = cu_seqlens_q;
+  p.cu_seqlens_k = cu_seqlens_k;
+  p.block_tables = block_tables;
+  const int64_t units = num_tokens + (int64_t)num_table_rows * max_table_len + num_plain + (n_var > 0 ? n_var + 1 : 0);
+  return launch_status(nvamd::launch_build_metadata(p, units, (hipStream_t)stream), fn);
+}
+
 int64_t nvamd_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t num_kv_heads,
                                      int32_t max_num_blocks, int32_t block_size, int32_t part_tokens) {
   if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || max_num_blocks <= 0 || block_size <= 0)

@@ -106,6 +106,22 @@ struct QkNormRopeParams {
 
 hipError_t launch_qk_norm_rope_store(const QkNormRopeParams& p, hipStream_t stream);
 
+// On-device attention metadata (see attn_metadata.hip).
+constexpr int kMetaMaxSeqs = 2048;
+struct AttnMetaParams {
+  const int32_t* packed;  // int32 [num_seqs, 4] descriptors, then the block tables back to back
+  int64_t packed_ints;    // int32 entries in packed
+  int num_seqs, num_plain, block_size, max_table_len;
+  int64_t cap_tokens, cap_slots, cap_rows;  // output sizes (writes beyond them are dropped)
+  int64_t* positions;
+  int32_t* slot_mapping;
+  int32_t* context_lens;
+  int32_t* cu_seqlens_q;
+  int32_t* cu_seqlens_k;
+  int32_t* block_tables;
+};
+hipError_t launch_build_metadata(const AttnMetaParams& p, int64_t units, hipStream_t stream);
+
 // FP8 block-scaled linear (128 x 128 weight blocks, 128-wide activation groups).
 struct Fp8GemmParams {
   const uint8_t* xq;        // E4M3FN [M, K], row stride K

@@ -39,6 +39,9 @@ SIGNATURES = {
     "nvamd_fp8_decode_attention_noalloc": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                                   _c_void_p, _i32, _i32, _i32, _i32, _i64, _i32, _i32,
                                                   _f32, _c_void_p]),
+    "nvamd_build_attention_metadata": (_i32, [_c_void_p, _i64, _i32, _i32, _i32, _i64, _i64, _i32, _i32,
+                                              _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                              _c_void_p]),
     "nvamd_fp8_act_quant": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _i64, _i64, _c_void_p]),
     "nvamd_fp8_block_gemm": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i32,
                                     _i64, _i64, _i64, _c_void_p]),

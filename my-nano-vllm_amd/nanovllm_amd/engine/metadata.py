@@ -20,7 +20,16 @@ memory with non-blocking copies (as the reference does, :141, :183-184,
 ``Seq``-like inputs need ``len(seq)``, ``num_cached_tokens``,
 ``num_scheduled_tokens`` and ``block_table`` -- nano-vLLM's ``Sequence``
 qualifies.
+
+``prepare_sequence_device`` builds the same tensors on the GPU instead: the
+host packs one int32 descriptor per sequence ``{num_tokens, num_cached,
+num_scheduled, len(block_table)}`` and the block tables back to back (work in
+the number of sequences and blocks, none per token), uploads it with one
+pinned non-blocking copy, and ``nvamd_build_attention_metadata`` expands it
+into positions, slot mapping, context lengths, cu_seqlens and the padded
+block tables.
 """
+import itertools
 from dataclasses import dataclass
 
 import numpy as np
@@ -138,3 +147,94 @@ def prepare_sequence(dseqs, pseqs, block_size, device="cuda"):
         max_seqlen_q=md.max_seqlen_q, max_seqlen_k=md.max_seqlen_k,
         block_tables=_to_device(md.block_tables, device))
     return _to_device(md.positions, device)
+
+
+@dataclass
+class PackedStep:
+    """One step's upload for the on-device build and the output sizes it implies."""
+    packed: np.ndarray       # int32: [num_seqs, 4] descriptors, then the block tables back to back
+    num_seqs: int
+    num_plain: int
+    num_spec: int
+    num_tokens: int          # positions
+    num_slots: int           # slot_mapping entries
+    num_table_rows: int      # sequences with a non-empty block table
+    max_table_len: int
+    max_seqlen_q: int
+    max_seqlen_k: int
+
+
+def pack_step(dseqs, pseqs, block_size) -> PackedStep:
+    """Orders the sequences as the reference does (plain decode, speculative,
+    prefill: model_runner.py:205-216) and packs their descriptors and block
+    tables.  Raises where the reference's loops would fail: a plain decode
+    sequence without a block table (``block_table[-1]``, :198), or a varlen
+    sequence whose table does not cover its scheduled positions (:175-181)."""
+    nd = [s for s in dseqs if s.num_scheduled_tokens == 1]
+    sd = [s for s in dseqs if s.num_scheduled_tokens > 1]
+    seqs = nd + sd + list(pseqs)
+    n = len(seqs)
+    desc = np.empty((n, 4), dtype=np.int64)
+    desc[:, 0] = np.fromiter((_seq_len(s) for s in seqs), dtype=np.int64, count=n)
+    desc[:, 1] = np.fromiter((s.num_cached_tokens for s in seqs), dtype=np.int64, count=n)
+    desc[:, 2] = np.fromiter((s.num_scheduled_tokens for s in seqs), dtype=np.int64, count=n)
+    desc[:, 3] = np.fromiter((len(s.block_table) if s.block_table else 0 for s in seqs), dtype=np.int64, count=n)
+    n_plain = len(nd)
+    tl = desc[:, 3]
+    if n_plain and (tl[:n_plain] == 0).any():
+        raise ValueError("a plain decode sequence has no block table")
+    var = desc[n_plain:]
+    ends = var[:, 1] + var[:, 2]
+    has = var[:, 3] > 0
+    if (has & ((ends + block_size - 1) // block_size > var[:, 3])).any():
+        raise ValueError("a varlen sequence's block table does not cover its scheduled positions")
+    total = int(tl.sum())
+    tables = np.fromiter(itertools.chain.from_iterable(s.block_table for s in seqs if s.block_table),
+                         dtype=np.int32, count=total)
+    packed = np.concatenate([desc.astype(np.int32).reshape(-1), tables])
+    return PackedStep(
+        packed=packed, num_seqs=n, num_plain=n_plain, num_spec=len(sd),
+        num_tokens=n_plain + int(var[:, 2].sum()),
+        num_slots=n_plain + int(var[has, 2].sum()),
+        num_table_rows=int((tl > 0).sum()), max_table_len=int(tl.max()) if n else 0,
+        max_seqlen_q=int(var[:, 2].max()) if len(var) else 0,
+        max_seqlen_k=int(ends.max()) if len(var) else 0)
+
+
+def build_device_metadata(step: PackedStep, block_size, device="cuda"):
+    """Uploads a packed step and builds its tensors on the GPU (on torch's
+    current stream).  Returns a dict with the fields nano-vLLM's Context
+    receives plus ``positions``."""
+    from .. import _native
+    dev = torch.device(device)
+    if dev.type != "cuda":
+        raise ValueError(f"the on-device build needs a ROCm GPU (got {device})")
+    lib = _native.load()
+    n_var = step.num_seqs - step.num_plain
+    packed = torch.from_numpy(step.packed).pin_memory().to(dev, non_blocking=True)
+    i32 = dict(dtype=torch.int32, device=dev)
+    positions = torch.empty(step.num_tokens, dtype=torch.int64, device=dev)
+    slot_mapping = torch.empty(step.num_slots, **i32)
+    context_lens = torch.empty(step.num_plain, **i32) if step.num_plain else None
+    cu_q = torch.empty(n_var + 1, **i32) if n_var else None
+    cu_k = torch.empty(n_var + 1, **i32) if n_var else None
+    tables = torch.empty(step.num_table_rows, step.max_table_len, **i32) if step.num_table_rows else None
+    ptr = lambda t: t.data_ptr() if t is not None else None  # noqa: E731
+    st = lib.nvamd_build_attention_metadata(
+        packed.data_ptr(), packed.numel(), step.num_seqs, step.num_plain, block_size, step.num_tokens,
+        step.num_slots, step.num_table_rows, step.max_table_len, positions.data_ptr(), ptr(slot_mapping),
+        ptr(context_lens), ptr(cu_q), ptr(cu_k), ptr(tables), torch.cuda.current_stream(dev).cuda_stream)
+    _native.check(st, "build_attention_metadata")
+    return dict(positions=positions, slot_mapping=slot_mapping, context_lens=context_lens,
+                cu_seqlens_q=cu_q, cu_seqlens_k=cu_k, max_seqlen_q=step.max_seqlen_q,
+                max_seqlen_k=step.max_seqlen_k, block_tables=tables, split_pt=step.num_plain,
+                num_spec_seqs=step.num_spec)
+
+
+def prepare_sequence_device(dseqs, pseqs, block_size, device="cuda"):
+    """prepare_sequence with the metadata built on the GPU: publishes it
+    through the Context and returns the device positions."""
+    md = build_device_metadata(pack_step(dseqs, pseqs, block_size), block_size, device)
+    positions = md.pop("positions")
+    set_context(**md)
+    return positions

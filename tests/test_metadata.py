@@ -102,3 +102,34 @@ def test_context_set_and_reset():
     assert c.split_pt == 3 and c.num_spec_seqs == 2     # unpassed fields keep their value
     ctxmod.reset_context()
     assert c.split_pt == 0 and c.num_spec_seqs == 0 and c.max_seqlen_q == 0
+
+
+@settings(max_examples=200, deadline=None)
+@given(batches())
+def test_pack_step_sizes_match_oracle(batch):
+    """The on-device build's upload: descriptors in the reference's row order,
+    tables back to back, and output sizes equal to the oracle's lengths."""
+    dseqs, pseqs = batch
+    if not dseqs and not pseqs:
+        return
+    want = om.prepare_sequence(dseqs, pseqs, BS)
+    st_ = nm.pack_step(dseqs, pseqs, BS)
+    order = [s for s in dseqs if s.num_scheduled_tokens == 1] + \
+            [s for s in dseqs if s.num_scheduled_tokens > 1] + pseqs
+    desc = st_.packed[:4 * len(order)].reshape(-1, 4)
+    assert desc.tolist() == [[s.num_tokens, s.num_cached_tokens, s.num_scheduled_tokens, len(s.block_table)]
+                             for s in order]
+    assert st_.packed[4 * len(order):].tolist() == [b for s in order for b in s.block_table]
+    assert st_.num_tokens == len(want["positions"]) and st_.num_slots == len(want["slot_mapping"])
+    assert st_.num_plain == want["split_pt"] and st_.num_spec == want["num_spec_seqs"]
+    rows = want["block_tables"] or []
+    assert st_.num_table_rows == len(rows) and (not rows or st_.max_table_len == len(rows[0]))
+    assert (st_.max_seqlen_q, st_.max_seqlen_k) == (want["max_seqlen_q"], want["max_seqlen_k"])
+
+
+def test_pack_step_rejects_what_the_reference_cannot_index():
+    import pytest
+    with pytest.raises(ValueError, match="plain decode"):
+        nm.pack_step([om.SeqView(10, 9, 1, [])], [], BS)
+    with pytest.raises(ValueError, match="does not cover"):
+        nm.pack_step([], [om.SeqView(600, 0, 600, [1, 2])], BS)
