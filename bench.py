@@ -45,7 +45,11 @@ Secondary fields in the same JSON line:
                and for the 16 x 512 prefill step: host time per call and time
                to completion of the on-device build and of the vectorised host
                build, the on-device build's GPU time, and, as CPU baseline,
-               the reference's own per-token loops and per-tensor copies.
+               the reference's own per-token loops and per-tensor copies;
+  lm_head      the sampler over the mixed step's 355 LM-head rows (Qwen3
+               vocabulary, bf16 logits) in GB/s of logits vs HBM, beside the
+               reference's arithmetic as eager torch ops, and the LM-head row
+               selection.
 These are timed after 0.15 s of sustained warm-up calls (the shader clock
 settles lower under continuous MFMA load within the first tens of
 milliseconds); the headline decode field runs exactly --warmup warm-up calls.
@@ -67,7 +71,7 @@ parity tests' checker) on the host cores for a bounded sample of the same
 workload; the prefill field carries one of its own.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--only decode|decode06|prefill|long|store|mixed|linear|metadata|all]
+                    [--only decode|decode06|prefill|long|store|mixed|linear|metadata|lm_head|all]
                     [--no-cpu-baseline]
                     [--copy-probe]
 """
@@ -108,7 +112,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", default="all",
-                    choices=["decode", "decode06", "prefill", "long", "store", "mixed", "linear", "metadata", "all"])
+                    choices=["decode", "decode06", "prefill", "long", "store", "mixed", "linear", "metadata", "lm_head",
+                             "all"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 1 GiB device copy (counter scale for rocprofv3 --pmc)")
@@ -358,6 +363,60 @@ def _blas_threads():
     except Exception:  # noqa: BLE001
         pass
     return os.cpu_count() or 1
+
+
+def bench_sampler(rows, vocab, steps, warmup):
+    """Temperature sampling of `rows` bf16 logit rows: the HIP sampler (in-kernel
+    Philox noise) and the reference's arithmetic as eager torch ops on the same
+    GPU (float copy, divide, softmax, exponential_, divide, argmax)."""
+    from nanovllm_amd.layers.sampler import sample_tokens
+    g = torch.Generator(device="cuda").manual_seed(rows)
+    logits = [(torch.randn(rows, vocab, device="cuda", generator=g) * 3).to(torch.bfloat16) for _ in range(2)]
+    temps = torch.rand(rows, device="cuda", generator=g) + 0.5
+
+    def ours(i):
+        sample_tokens(logits[i & 1], temps, seed=i)
+
+    def torch_ref(i):
+        y = logits[i & 1].float().div_(temps.unsqueeze(1))
+        p = torch.softmax(y, dim=-1)
+        p.div_(torch.empty_like(p).exponential_(1).clamp_min_(1e-10)).argmax(dim=-1)
+
+    ms = timed(ours, steps, warmup)
+    ms_ref = timed(torch_ref, max(steps // 2, 5), max(warmup // 2, 2))
+    nbytes = rows * vocab * 2
+    return dict(ms=ms, gbs=nbytes / (ms * 1e-3) / 1e9, ms_torch=ms_ref, bytes=nbytes)
+
+
+def bench_select_rows(steps, warmup):
+    """LM-head row selection of the mixed step: 192 decode + 32 x 5 speculative
+    rows + 3 prefill chunks of 512 (their last rows), hidden 4096, bf16."""
+    from nanovllm_amd.layers.embed_head import select_lm_head_rows
+    from nanovllm_amd.utils.context import set_context, reset_context
+    lq = [5] * 32 + [512] * 3
+    cu = [0] + list(np.cumsum(lq))
+    x = torch.randn(192 + cu[-1], 4096, device="cuda").to(torch.bfloat16)
+    set_context(split_pt=192, num_spec_seqs=32, num_spec_rows=160,
+                cu_seqlens_q=torch.tensor(cu, dtype=torch.int32, device="cuda"))
+    try:
+        ms = timed(lambda i: select_lm_head_rows(x), steps, warmup)
+    finally:
+        reset_context()
+    return dict(ms=ms, rows=192 + 160 + 3)
+
+
+def cpu_baseline_sampler(vocab, rows=8, target_s=6.0):
+    from oracle import lm_head as olh
+    rng = np.random.default_rng(0)
+    logits = rng.normal(size=(rows, vocab)).astype(np.float32)
+    temps = np.ones(rows, np.float32)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < target_s or n == 0:
+        olh.sample(logits, temps, olh.exponential_noise(n, 0, rows, vocab))
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    return dict(value=round(rows * vocab * 2 / dt / 1e9, 3), unit="GB/s of bf16 logits", cores=1, kind="port",
+                sample=f"oracle Philox noise + sample on {rows} rows x {vocab}, {n} runs")
 
 
 class _StepSeq:
@@ -718,6 +777,23 @@ def main():
                 f"{res['host_numpy']['host_us']:.1f} / {res['host_numpy']['to_completion_us']:.1f} us")
         extra["metadata"] = dict(workload="one engine step's attention metadata (mixed batch; 16 x 512 prefill)",
                                  kernels="build_metadata_kernel", **out)
+
+    if args.only in ("lm_head", "all"):
+        res = bench_sampler(355, 151936, max(args.steps, 20), max(args.warmup, 5))
+        sel = bench_select_rows(max(args.steps, 20), max(args.warmup, 5))
+        log(f"sampler: {res['ms'] * 1e3:.1f} us ({res['gbs']:.0f} GB/s), reference arithmetic in torch "
+            f"{res['ms_torch'] * 1e3:.1f} us; row selection {sel['ms'] * 1e3:.1f} us")
+        extra["lm_head"] = dict(
+            workload="the mixed step's LM-head rows (192 decode + 32 x 5 speculative + 3 prefill = 355), "
+                     "Qwen3 vocabulary 151936, bf16 logits",
+            kernels="sample_kernel, select_rows_kernel",
+            sampler=dict(ms_per_step=round(res["ms"], 5), gbs=round(res["gbs"], 1),
+                         frac_hbm_peak=round(res["gbs"] / HBM_PEAK_GBS, 4), algorithmic_bytes=res["bytes"],
+                         reference_arithmetic_torch_ms=round(res["ms_torch"], 5)),
+            select_rows=dict(ms_per_step=round(sel["ms"], 5), rows=sel["rows"]))
+        if not args.no_cpu_baseline:
+            extra["lm_head"]["cpu_baseline"] = cpu_baseline_sampler(151936)
+        torch.cuda.empty_cache()
 
     if "value" not in line:   # partial runs (profiling) still print one line
         first = next(iter(extra.values()))

@@ -1,6 +1,6 @@
-// C ABI entry points (declared in include/nvamd_fp8_attention.h and
-// include/nvamd_fp8_linear.h): argument validation, static partition sizing
-// and kernel launches.
+// C ABI entry points (declared in include/nvamd_fp8_attention.h,
+// include/nvamd_fp8_linear.h and include/nvamd_lm_head.h): argument
+// validation, static partition sizing and kernel launches.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -13,6 +13,7 @@
 #include "kernels.h"
 #include "nvamd_fp8_attention.h"
 #include "nvamd_fp8_linear.h"
+#include "nvamd_lm_head.h"
 
 // Scratch of nvamd_fp8_decode_attention_noalloc: device memory the library
 // holds for the whole process on every GPU it runs on (each GPU has its own
@@ -377,6 +378,62 @@ int32_t nvamd_build_attention_metadata(const int32_t* packed, int64_t packed_int
   p.block_tables = block_tables;
   const int64_t units = num_tokens + (int64_t)num_table_rows * max_table_len + num_plain + (n_var > 0 ? n_var + 1 : 0);
   return launch_status(nvamd::launch_build_metadata(p, units, (hipStream_t)stream), fn);
+}
+
+// Workgroups per sampled row: about two per CU over the call, 1 .. 32.
+static int64_t sample_parts(int64_t rows) {
+  const int64_t cus = device_cu_count();
+  return std::min<int64_t>(32, std::max<int64_t>(1, (2 * cus + rows - 1) / rows));
+}
+
+int32_t nvamd_select_logit_rows(const void* x, int64_t x_stride0, int64_t x_rows, int32_t hidden, int32_t elem_bytes,
+                                const int32_t* cu_seqlens_q, int32_t num_plain, int32_t num_spec_seqs,
+                                int32_t num_spec_rows, int32_t num_prefill_seqs, void* out, int64_t out_stride0,
+                                void* stream) {
+  static const char* fn = "select_logit_rows";
+  if (x_rows < 0 || hidden <= 0 || (elem_bytes != 2 && elem_bytes != 4) || num_plain < 0 || num_spec_seqs < 0 ||
+      num_spec_rows < 0 || num_prefill_seqs < 0 || x_stride0 < hidden || out_stride0 < hidden)
+    return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: bad sizes", fn);
+  const int64_t out_rows = (int64_t)num_plain + num_spec_rows + num_prefill_seqs;
+  if ((int64_t)num_plain + num_spec_rows > x_rows)
+    return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: %lld kept prefix rows exceed the %lld rows of x", fn,
+                (long long)((int64_t)num_plain + num_spec_rows), (long long)x_rows);
+  if (out_rows == 0) return ok();
+  if (!x || !out || (num_prefill_seqs > 0 && !cu_seqlens_q)) return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+  const int64_t row_bytes = (int64_t)hidden * elem_bytes;
+  if (row_bytes % 16 != 0 || row_bytes > 0x7fffffff || (uintptr_t)x % 16 != 0 || (uintptr_t)out % 16 != 0 ||
+      (x_stride0 * elem_bytes) % 16 != 0 || (out_stride0 * elem_bytes) % 16 != 0)
+    return fail(NVAMD_ERR_UNSUPPORTED, "%s: rows must be whole 16-byte units, 16-byte aligned", fn);
+  return launch_status(nvamd::launch_select_rows(x, x_stride0 * elem_bytes, x_rows, (int)row_bytes, cu_seqlens_q,
+                                                 num_plain, num_spec_rows, num_spec_seqs, out_rows, out,
+                                                 out_stride0 * elem_bytes, (hipStream_t)stream),
+                       fn);
+}
+
+int64_t nvamd_sample_workspace_bytes(int64_t rows) {
+  if (rows <= 0 || rows > 0x7fffffff) return 0;
+  return sample_parts(rows) * rows * 16;
+}
+
+int32_t nvamd_sample(const void* logits, int32_t logits_dtype, int64_t stride0, int64_t rows, int64_t vocab,
+                     const float* temperatures, const float* noise, uint64_t seed, uint64_t offset, int64_t* out,
+                     void* workspace, int64_t workspace_bytes, void* stream) {
+  static const char* fn = "sample";
+  if (rows < 0 || rows > 0x7fffffff || vocab <= 0 || vocab > (1ll << 40) || stride0 < vocab ||
+      logits_dtype < NVAMD_LOGITS_BF16 || logits_dtype > NVAMD_LOGITS_F32)
+    return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: bad sizes or dtype (rows=%lld vocab=%lld dtype=%d)", fn,
+                (long long)rows, (long long)vocab, logits_dtype);
+  if (rows == 0) return ok();
+  if (!logits || !temperatures || !out) return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+  const int parts = sample_parts(rows);
+  if (workspace == nullptr || workspace_bytes < parts * rows * 16 || (uintptr_t)workspace % 16 != 0)
+    return fail(NVAMD_ERR_WORKSPACE, "%s: workspace of %lld bytes (16-byte aligned) needed", fn,
+                (long long)(parts * rows * 16));
+  float* part_score = static_cast<float*>(workspace);
+  int64_t* part_index = reinterpret_cast<int64_t*>(static_cast<char*>(workspace) + ((parts * rows * 4 + 15) & ~15ll));
+  return launch_status(nvamd::launch_sample(logits, logits_dtype, stride0, rows, vocab, temperatures, noise, seed,
+                                            offset, out, part_score, part_index, (int)parts, (hipStream_t)stream),
+                       fn);
 }
 
 int64_t nvamd_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t num_kv_heads,

@@ -23,7 +23,7 @@ _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64
 _f32 = ctypes.c_float
 
-# name -> (restype, argtypes); mirrors include/nvamd_fp8_attention.h and include/nvamd_fp8_linear.h
+# name -> (restype, argtypes); mirrors include/nvamd_fp8_attention.h, nvamd_fp8_linear.h and nvamd_lm_head.h
 SIGNATURES = {
     "nvamd_abi_version": (_i32, []),
     "nvamd_last_error": (ctypes.c_char_p, []),
@@ -42,6 +42,11 @@ SIGNATURES = {
     "nvamd_build_attention_metadata": (_i32, [_c_void_p, _i64, _i32, _i32, _i32, _i64, _i64, _i32, _i32,
                                               _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                               _c_void_p]),
+    "nvamd_select_logit_rows": (_i32, [_c_void_p, _i64, _i64, _i32, _i32, _c_void_p, _i32, _i32, _i32, _i32,
+                                       _c_void_p, _i64, _c_void_p]),
+    "nvamd_sample_workspace_bytes": (_i64, [_i64]),
+    "nvamd_sample": (_i32, [_c_void_p, _i32, _i64, _i64, _i64, _c_void_p, _c_void_p, ctypes.c_uint64,
+                            ctypes.c_uint64, _c_void_p, _c_void_p, _i64, _c_void_p]),
     "nvamd_fp8_act_quant": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _i64, _i64, _c_void_p]),
     "nvamd_fp8_block_gemm": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i32,
                                     _i64, _i64, _i64, _c_void_p]),

@@ -138,8 +138,9 @@ def prepare_sequence(dseqs, pseqs, block_size, device="cuda"):
     the device positions (model_runner.prepare_sequence, :203-220)."""
     md = build_host_metadata(dseqs, pseqs, block_size)
     has_varlen = md.cu_seqlens_q.size > 0
+    num_spec_rows = sum(s.num_scheduled_tokens for s in dseqs if s.num_scheduled_tokens > 1)
     set_context(
-        split_pt=md.split_pt, num_spec_seqs=md.num_spec_seqs,
+        split_pt=md.split_pt, num_spec_seqs=md.num_spec_seqs, num_spec_rows=num_spec_rows,
         slot_mapping=_to_device(md.slot_mapping, device),
         context_lens=_to_device(md.context_lens, device) if md.split_pt else None,
         cu_seqlens_q=_to_device(md.cu_seqlens_q, device) if has_varlen else None,
@@ -162,6 +163,7 @@ class PackedStep:
     max_table_len: int
     max_seqlen_q: int
     max_seqlen_k: int
+    num_spec_rows: int       # query rows of the speculative sequences
 
 
 def pack_step(dseqs, pseqs, block_size) -> PackedStep:
@@ -198,7 +200,8 @@ def pack_step(dseqs, pseqs, block_size) -> PackedStep:
         num_slots=n_plain + int(var[has, 2].sum()),
         num_table_rows=int((tl > 0).sum()), max_table_len=int(tl.max()) if n else 0,
         max_seqlen_q=int(var[:, 2].max()) if len(var) else 0,
-        max_seqlen_k=int(ends.max()) if len(var) else 0)
+        max_seqlen_k=int(ends.max()) if len(var) else 0,
+        num_spec_rows=int(desc[n_plain:n_plain + len(sd), 2].sum()))
 
 
 def build_device_metadata(step: PackedStep, block_size, device="cuda"):
@@ -228,7 +231,7 @@ def build_device_metadata(step: PackedStep, block_size, device="cuda"):
     return dict(positions=positions, slot_mapping=slot_mapping, context_lens=context_lens,
                 cu_seqlens_q=cu_q, cu_seqlens_k=cu_k, max_seqlen_q=step.max_seqlen_q,
                 max_seqlen_k=step.max_seqlen_k, block_tables=tables, split_pt=step.num_plain,
-                num_spec_seqs=step.num_spec)
+                num_spec_seqs=step.num_spec, num_spec_rows=step.num_spec_rows)
 
 
 def prepare_sequence_device(dseqs, pseqs, block_size, device="cuda"):

@@ -4,6 +4,9 @@ Same fields, defaults and setter semantics as nanovllm/utils/context.py:5-48:
 ``split_pt`` separates plain-decode rows (before) from varlen rows (after),
 ``num_spec_seqs`` counts the speculative sequences at the front of the varlen
 group, and the tensors are int32 device tensors (block tables padded with -1).
+One field is added to the reference's: ``num_spec_rows``, the host-side count
+of the speculative sequences' query rows (``cu_seqlens_q[num_spec_seqs]``),
+which the metadata builders know; -1 when unknown.
 """
 from dataclasses import dataclass
 
@@ -21,6 +24,7 @@ class Context:
     slot_mapping: torch.Tensor | None = None
     context_lens: torch.Tensor | None = None
     block_tables: torch.Tensor | None = None
+    num_spec_rows: int = -1
 
 
 _CONTEXT = Context()
@@ -34,11 +38,12 @@ def get_context() -> Context:
 
 def set_context(split_pt=_UNSET, num_spec_seqs=_UNSET, cu_seqlens_q=_UNSET, cu_seqlens_k=_UNSET,
                 max_seqlen_q=_UNSET, max_seqlen_k=_UNSET, slot_mapping=_UNSET,
-                context_lens=_UNSET, block_tables=_UNSET):
+                context_lens=_UNSET, block_tables=_UNSET, num_spec_rows=_UNSET):
     """Updates only the fields that are passed (unpassed fields keep their value)."""
     values = dict(split_pt=split_pt, num_spec_seqs=num_spec_seqs, cu_seqlens_q=cu_seqlens_q,
                   cu_seqlens_k=cu_seqlens_k, max_seqlen_q=max_seqlen_q, max_seqlen_k=max_seqlen_k,
-                  slot_mapping=slot_mapping, context_lens=context_lens, block_tables=block_tables)
+                  slot_mapping=slot_mapping, context_lens=context_lens, block_tables=block_tables,
+                  num_spec_rows=num_spec_rows)
     for name, value in values.items():
         if value is not _UNSET:
             setattr(_CONTEXT, name, value)
