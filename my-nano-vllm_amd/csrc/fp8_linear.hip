@@ -251,20 +251,23 @@ __global__ __launch_bounds__(64 * WN * WM) void block_gemm_kernel(Fp8GemmParams 
 }
 
 // Tile configurations, largest first: (WN, WM, TN, TM) -> BN x BM.
-//   0: 2 x 2 waves, 4 x 2 fragments -> 128 features x 64 tokens
-//   1: 4 x 1 waves, 2 x 2 fragments -> 128 x 32
-//   2: 2 x 1 waves, 2 x 1 fragments ->  64 x 16
-// (A 256 x 128 tile on 2 x 2 waves of 8 x 4 fragments was slower than 0 at
-// every size measured, M = 192 .. 8192: with one workgroup per CU its double
-// buffer cannot hide the tile loads.)
-constexpr int kGemmConfigs = 3;
-constexpr int kGemmBN[kGemmConfigs] = {128, 128, 64};
-constexpr int kGemmBM[kGemmConfigs] = {64, 32, 16};
+//   0: 2 x 4 waves, 8 x 4 fragments -> 256 features x 256 tokens (one
+//      workgroup of 8 waves per CU: a K block is ~1 us of MFMA work, about
+//      the latency of the next block's loads, which the second buffer hides)
+//   1: 2 x 2 waves, 4 x 2 fragments -> 128 x 64
+//   2: 4 x 1 waves, 2 x 2 fragments -> 128 x 32
+//   3: 2 x 1 waves, 2 x 1 fragments ->  64 x 16
+// (A 256 x 128 tile on 4 waves was slower than 1 at every size measured:
+// with one wave per SIMD neither the loads nor the FMAs overlap the MFMAs.)
+constexpr int kGemmConfigs = 4;
+constexpr int kGemmBN[kGemmConfigs] = {256, 128, 128, 64};
+constexpr int kGemmBM[kGemmConfigs] = {256, 64, 32, 16};
 
 int64_t config_lds_bytes(int c, int Kc) {
   switch (c) {
-    case 0: return gemm_lds_bytes<2, 2, 4, 2>(Kc);
-    case 1: return gemm_lds_bytes<4, 1, 2, 2>(Kc);
+    case 0: return gemm_lds_bytes<2, 4, 8, 4>(Kc);
+    case 1: return gemm_lds_bytes<2, 2, 4, 2>(Kc);
+    case 2: return gemm_lds_bytes<4, 1, 2, 2>(Kc);
     default: return gemm_lds_bytes<2, 1, 2, 1>(Kc);
   }
 }
@@ -322,11 +325,13 @@ hipError_t launch_fp8_block_gemm(const Fp8GemmParams& p, int config, bool f16_ou
     return hipErrorInvalidValue;
   const int64_t lds = config_lds_bytes(config, p.Kc);
   switch (config * 2 + (f16_out ? 1 : 0)) {
-    case 0: return launch_config<2, 2, 4, 2, false>(p, lds, stream);
-    case 1: return launch_config<2, 2, 4, 2, true>(p, lds, stream);
-    case 2: return launch_config<4, 1, 2, 2, false>(p, lds, stream);
-    case 3: return launch_config<4, 1, 2, 2, true>(p, lds, stream);
-    case 4: return launch_config<2, 1, 2, 1, false>(p, lds, stream);
+    case 0: return launch_config<2, 4, 8, 4, false>(p, lds, stream);
+    case 1: return launch_config<2, 4, 8, 4, true>(p, lds, stream);
+    case 2: return launch_config<2, 2, 4, 2, false>(p, lds, stream);
+    case 3: return launch_config<2, 2, 4, 2, true>(p, lds, stream);
+    case 4: return launch_config<4, 1, 2, 2, false>(p, lds, stream);
+    case 5: return launch_config<4, 1, 2, 2, true>(p, lds, stream);
+    case 6: return launch_config<2, 1, 2, 1, false>(p, lds, stream);
     default: return launch_config<2, 1, 2, 1, true>(p, lds, stream);
   }
 }

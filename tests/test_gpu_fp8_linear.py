@@ -15,8 +15,8 @@ largest error seen is 2^-15 of the sum of absolute terms; a misplaced or
 missing K block errs by about 2^-3.5 of it.
 
 Shapes are chosen so that on a 256-CU MI355X the library picks each of its
-tile shapes (128x64, 128x32, 64x16 features x tokens): it takes the largest
-tile whose grid still covers the CUs.
+tile shapes (256x256, 128x64, 128x32, 64x16 features x tokens): it takes the
+largest tile whose grid still covers the CUs.
 """
 import numpy as np
 import pytest
@@ -132,9 +132,9 @@ def test_act_quant_unit_scale_all_patterns_and_strided_rows():
     assert np.array_equal(_bits(xs), xs_ref)
 
 
-# (M, N, K): tile chosen on 256 CUs -> 128x64: (2048, 4096, 256), (1024, 2048, 256);
+# (M, N, K): tile chosen on 256 CUs -> 256x256: (4096, 4096, 256); 128x64: (1024, 2048, 256);
 # 128x32: (1024, 1024, 128); 64x16: the small shapes
-TILE_SHAPES = [(2048, 4096, 256), (1024, 2048, 256), (1024, 1024, 128), (24, 256, 512), (1, 128, 128)]
+TILE_SHAPES = [(4096, 4096, 256), (1024, 2048, 256), (1024, 1024, 128), (24, 256, 512), (1, 128, 128)]
 
 
 @pytest.mark.parametrize("M,N,K", TILE_SHAPES)
@@ -154,7 +154,7 @@ def test_gemm_exact_integer_case(M, N, K):
     assert np.array_equal(_bits(got), want)
 
 
-@pytest.mark.parametrize("M,N,K,out_dtype", [(2048, 4096, 256, torch.bfloat16), (1000, 2048, 512, torch.bfloat16),
+@pytest.mark.parametrize("M,N,K,out_dtype", [(4000, 4096, 384, torch.bfloat16), (1000, 2048, 512, torch.bfloat16),
                                              (77, 1024, 1024, torch.float16), (5, 384, 4096, torch.bfloat16),
                                              (130, 256, 12288, torch.bfloat16)])
 def test_gemm_matches_oracle(M, N, K, out_dtype):
