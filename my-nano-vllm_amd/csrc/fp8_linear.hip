@@ -21,10 +21,14 @@
 // activation scale per fragment column and one weight scale per 128
 // features: acc += P * (sx * sw), one FMA per output per K block.  W and X
 // tiles ([rows x 128 B] per K block) are staged through LDS by direct-to-LDS
-// 16-byte loads (two buffers), rows' 16-byte granules XOR-swizzled by row so
-// that the fragment reads (16 rows, 32 B per lane) are bank-conflict free.
-// The activation scales of the tile's tokens ([BM x Kc] bf16, contiguous in
-// x_scale) and the weight scales of its feature blocks are loaded to LDS once.
+// 16-byte loads, rows' 16-byte granules XOR-swizzled by row so that the
+// fragment reads (16 rows, 32 B per lane) are bank-conflict free.  Two stage
+// buffers and one barrier per K block: the barrier that publishes stage kc
+// also retires stage kc - 1, so stage kc + 1 is issued into its buffer right
+// after it and loads while stage kc is computed.  A stage also holds, per
+// token row, the x_scale dword with the row's scale for the K block (one
+// direct-to-LDS dword load per 64 rows); the weight scales of the tile's
+// feature blocks ([kWBlocks x Kc]) are loaded to LDS once.
 // A lane feeds the MFMA the bytes of K-chunk lane / 16 (32 bytes) of its row
 // in both operands, so any assignment of K positions to (lane, byte) that
 // the hardware uses for A it also uses for B, and the sum over K is exact
@@ -100,14 +104,16 @@ struct GemmTile {
   static constexpr int BM = 16 * TM * WM;
   static constexpr int kWBytes = BN * kFp8Block;   // one K block of the weight tile
   static constexpr int kXBytes = BM * kFp8Block;   // one K block of the activation tile
-  static constexpr int kStage = kWBytes + kXBytes;
+  static constexpr int kSxLoads = (BM + 63) / 64;   // dword loads (64 rows each) of a K block's activation scales
+  static constexpr int kSxBytes = 256 * kSxLoads;
+  static constexpr int kStage = kWBytes + kXBytes + kSxBytes;
   static constexpr int kWLoads = kWBytes / 1024 / kWaves;  // 1 KiB loads per wave per stage
   static constexpr int kXLoads = kXBytes / 1024 / kWaves;
   static constexpr int kLoads = kWLoads + kXLoads;
   static constexpr int kWBlocks = (BN + kFp8Block - 1) / kFp8Block;  // weight-scale rows spanned
   static_assert(kWBytes % (1024 * kWaves) == 0 && kXBytes % (1024 * kWaves) == 0, "whole loads per wave");
   static_assert(BN <= kFp8Block || BN % kFp8Block == 0, "a fragment never straddles two weight blocks");
-  static_assert(kLoads < 32, "vmcnt range");
+  static_assert(kWaves >= kSxLoads, "one scale load per wave");
 };
 
 template <int WN, int WM, int TN, int TM>
@@ -115,13 +121,14 @@ constexpr int64_t gemm_scale_offset() { return 2 * GemmTile<WN, WM, TN, TM>::kSt
 
 __host__ __device__ constexpr int64_t round_up_1k(int64_t b) { return (b + 1023) & ~(int64_t)1023; }
 
-// LDS bytes of a launch: two stages, then the activation scales [BM, Kc] and
-// the weight scales [kWBlocks, Kc] (bf16, the latter from up to 7 elements
-// earlier; each region rounded up to whole 1 KiB loads).
+// LDS bytes of a launch: two stages (weight tile, activation tile, and per
+// token row the dword of x_scale that holds its scale for the K block), then
+// the weight scales [kWBlocks, Kc] (bf16, from up to 7 elements earlier,
+// rounded up to whole 1 KiB loads).
 template <int WN, int WM, int TN, int TM>
 int64_t gemm_lds_bytes(int Kc) {
   using T = GemmTile<WN, WM, TN, TM>;
-  return 2 * T::kStage + round_up_1k((int64_t)T::BM * Kc * 2) + round_up_1k(((int64_t)T::kWBlocks * Kc + 8) * 2);
+  return 2 * T::kStage + round_up_1k(((int64_t)T::kWBlocks * Kc + 8) * 2);
 }
 
 // 8 swizzled fragment bytes -> MFMA operand: row r (16 rows), K-chunk q =
@@ -171,6 +178,8 @@ __global__ __launch_bounds__(64 * WN * WM) void block_gemm_kernel(Fp8GemmParams 
     const int r = 8 * (wave + T::kWaves * i) + fr;
     return (uint32_t)((int64_t)r * Kc * kFp8Block + kc * kFp8Block + 16 * (fp ^ (r & 7)));
   };
+  // wave w < kSxLoads: token rows 64 w + lane, the dword holding x_scale[row][kc]
+  const uint32_t sx_row_off = (uint32_t)((64 * wave + lane) * Kc) * 2u;
   auto issue_stage = [&](int kc, int buf) {
     const uint32_t base = lds0 + (uint32_t)(buf * T::kStage);
 #pragma unroll
@@ -179,18 +188,15 @@ __global__ __launch_bounds__(64 * WN * WM) void block_gemm_kernel(Fp8GemmParams 
 #pragma unroll
     for (int i = 0; i < T::kXLoads; ++i)
       dma_load16_keep(rx, x_off(i, kc), base + (uint32_t)(T::kWBytes + 1024 * (wave + T::kWaves * i)));
+    if (wave < T::kSxLoads)
+      dma_load4_keep(rsx, (sx_row_off + 2u * kc) & ~3u, base + (uint32_t)(T::kWBytes + T::kXBytes + 256 * wave));
   };
 
-  // scales: [BM x Kc] activation scales then [kWBlocks x Kc] weight scales
-  const uint32_t sx_lds = lds0 + (uint32_t)gemm_scale_offset<WN, WM, TN, TM>();
-  const int64_t sx_region = round_up_1k((int64_t)T::BM * Kc * 2);
-  const uint32_t sw_lds = sx_lds + (uint32_t)sx_region;
-  for (int i = wave; i < (int)(sx_region / 1024); i += T::kWaves)
-    dma_load16_keep(rsx, 1024u * i + 16u * lane, sx_lds + 1024u * i);
+  // weight scales [kWBlocks x Kc], loaded once
+  const uint32_t sw_lds = lds0 + (uint32_t)gemm_scale_offset<WN, WM, TN, TM>();
   for (int i = wave; i < (int)(round_up_1k(((int64_t)T::kWBlocks * Kc + 8) * 2) / 1024); i += T::kWaves)
     dma_load16_keep(rsw, 1024u * i + 16u * lane, sw_lds + 1024u * i);
   issue_stage(0, 0);
-  if (Kc > 1) issue_stage(1, 1);
 
   f32x4 acc[TN][TM];
 #pragma unroll
@@ -199,23 +205,28 @@ __global__ __launch_bounds__(64 * WN * WM) void block_gemm_kernel(Fp8GemmParams 
     for (int j = 0; j < TM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int q = lane >> 4, r16 = lane & 15;
-  const uint16_t* sx_rows = reinterpret_cast<const uint16_t*>(smem + gemm_scale_offset<WN, WM, TN, TM>());
-  const uint16_t* sw_rows = reinterpret_cast<const uint16_t*>(smem + gemm_scale_offset<WN, WM, TN, TM>() + sx_region);
+  const uint16_t* sw_rows = reinterpret_cast<const uint16_t*>(smem + gemm_scale_offset<WN, WM, TN, TM>());
   const int wblk = T::BN <= kFp8Block ? 0 : (wn * TN * 16) / kFp8Block;  // the wave's weight block in the tile
 
   for (int kc = 0; kc < Kc; ++kc) {
-    if (kc + 1 < Kc) wait_vmcnt<T::kLoads>();  // stage kc (and the scales) landed; kc + 1 may be in flight
-    else wait_vmcnt<0>();
+    // one barrier per K block: past it, every wave's loads of stage kc have
+    // landed and every wave is done reading buffer (kc + 1) & 1 (stage kc - 1),
+    // which then receives stage kc + 1 while stage kc is computed
+    wait_vmcnt<0>();  // this wave's loads of stage kc (and of the scales)
     lds_barrier();
+    if (kc + 1 < Kc) issue_stage(kc + 1, (kc + 1) & 1);
     const uint8_t* st = smem + (kc & 1) * T::kStage;
     const uint8_t* wrows = st + (wn * TN * 16) * kFp8Block;
     const uint8_t* xrows = st + T::kWBytes + (wm * TM * 16) * kFp8Block;
+    const uint32_t* sx_dw = reinterpret_cast<const uint32_t*>(st + T::kWBytes + T::kXBytes);
     const float sw = bf16_bits_to_f32(sw_rows[sw_shift + wblk * Kc + kc]);
     float s[TM];
     i32x8 b[TM];
 #pragma unroll
     for (int j = 0; j < TM; ++j) {
-      s[j] = bf16_bits_to_f32(sx_rows[(wm * TM * 16 + 16 * j + r16) * Kc + kc]) * sw;  // exact
+      const int row = wm * TM * 16 + 16 * j + r16;
+      const uint32_t d = sx_dw[row];
+      s[j] = bf16_bits_to_f32((row * Kc + kc) & 1 ? d >> 16 : d & 0xFFFFu) * sw;  // exact
       b[j] = read_frag(xrows + 16 * j * kFp8Block, r16, q);
     }
 #pragma unroll
@@ -229,8 +240,6 @@ __global__ __launch_bounds__(64 * WN * WM) void block_gemm_kernel(Fp8GemmParams 
         for (int e = 0; e < 4; ++e) acc[i][j][e] = __builtin_fmaf(part[e], s[j], acc[i][j][e]);
       }
     }
-    lds_barrier();  // every wave is done with buffer kc & 1
-    if (kc + 2 < Kc) issue_stage(kc + 2, kc & 1);
   }
 
   // out[m][n]: lane holds D[4 (lane / 16) + e][lane % 16] of each fragment,

@@ -53,6 +53,17 @@ __device__ __forceinline__ void dma_load16_keep(u32x4 rsrc, uint32_t voff, uint3
       : "s"(lds), "v"(voff), "s"(rsrc));
 }
 
+// Direct-to-LDS 4-byte load: lane l's dword at byte offset voff lands at LDS
+// address lds + 4*l (default cache policy; same conventions as above).
+__device__ __forceinline__ void dma_load4_keep(u32x4 rsrc, uint32_t voff, uint32_t lds) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dword %1, %2, 0 offen lds"
+      :
+      : "s"(lds), "v"(voff), "s"(rsrc));
+}
+
 // s_waitcnt vmcnt(n) (gfx9 encoding; expcnt and lgkmcnt left unconstrained).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {

@@ -132,9 +132,11 @@ def test_act_quant_unit_scale_all_patterns_and_strided_rows():
     assert np.array_equal(_bits(xs), xs_ref)
 
 
-# (M, N, K): tile chosen on 256 CUs -> 256x256: (4096, 4096, 256); 128x64: (1024, 2048, 256);
-# 128x32: (1024, 1024, 128); 64x16: the small shapes
-TILE_SHAPES = [(4096, 4096, 256), (1024, 2048, 256), (1024, 1024, 128), (24, 256, 512), (1, 128, 128)]
+# (M, N, K): tile chosen on 256 CUs -> 256x256: (4096, 4096, 256), and (4096, 4096, 640) with an odd
+# number of K blocks (a token row's scale then sits in either half of its x_scale dword);
+# 128x64: (1024, 2048, 256); 128x32: (1024, 1024, 128); 64x16: the small shapes
+TILE_SHAPES = [(4096, 4096, 256), (4096, 4096, 640), (1024, 2048, 256), (1024, 1024, 128), (24, 256, 512),
+               (1, 128, 128)]
 
 
 @pytest.mark.parametrize("M,N,K", TILE_SHAPES)
@@ -173,6 +175,32 @@ def test_gemm_matches_oracle(M, N, K, out_dtype):
     acc = torch.from_numpy(acc).double()
     ulp = 2.0 ** -7 if out_dtype == torch.bfloat16 else 2.0 ** -10
     bad = (got - acc).abs() > ulp * acc.abs() + ABS_TOL * absum
+    assert not bad.any(), f"{int(bad.sum())} outputs off, first at {bad.nonzero()[0].tolist()}"
+
+
+def test_gemm_large_tile_long_k_against_torch_fp32():
+    """The 256x256 tile at the Qwen3-8B down-projection depth (K = 12,288, 96
+    scale blocks; 4,000 tokens, ragged against the tile), against the same
+    block-scaled sum in torch fp32 on the GPU (per K block an fp32 matmul of
+    the dequantised codes, times x_scale * w_scale), at the oracle's
+    tolerance.  The full-size oracle would take minutes on the host."""
+    announce("fp8 linear: GEMM 4000 x 4096 x 12288 (256x256 tile) vs torch fp32")
+    g = torch.Generator().manual_seed(12288)
+    M, N, K = 4000, 4096, 12288
+    xq, w = _codes(g, (M, K)), _codes(g, (N, K))
+    x_scale, w_scale = _scales(g, (M, K // 128)), _scales(g, (N // 128, K // 128))
+    got = _gemm_gpu(xq, x_scale, w, w_scale).cuda().double()
+    t = torch.from_numpy(fp8.dequant_table().astype(np.float32)).cuda()
+    xd, wd = t[xq.cuda().long()], t[w.cuda().long()]
+    xs, ws = x_scale.cuda().float(), w_scale.cuda().float().repeat_interleave(128, 0)
+    acc = torch.zeros(M, N, device="cuda")
+    absum = torch.zeros(M, N, device="cuda")
+    for kc in range(K // 128):
+        xb, wb = xd[:, 128 * kc:128 * (kc + 1)], wd[:, 128 * kc:128 * (kc + 1)].T.contiguous()
+        s = xs[:, kc:kc + 1] * ws[:, kc][None, :]
+        acc += torch.matmul(xb, wb) * s
+        absum += torch.matmul(xb.abs(), wb.abs()) * s
+    bad = (got - acc.double()).abs() > 2.0 ** -7 * acc.double().abs() + ABS_TOL * absum.double()
     assert not bad.any(), f"{int(bad.sum())} outputs off, first at {bad.nonzero()[0].tolist()}"
 
 
