@@ -49,7 +49,10 @@ Secondary fields in the same JSON line:
   lm_head      the sampler over the mixed step's 355 LM-head rows (Qwen3
                vocabulary, bf16 logits) in GB/s of logits vs HBM, beside the
                reference's arithmetic as eager torch ops, and the LM-head row
-               selection.
+               selection;
+  host_overhead  host time per call of the Python entry points (checks,
+               workspace lookup, ctypes, launches) and of the bare C-ABI
+               decode call, with nothing synchronised in the loop.
 These are timed after 0.15 s of sustained warm-up calls (the shader clock
 settles lower under continuous MFMA load within the first tens of
 milliseconds); the headline decode field runs exactly --warmup warm-up calls.
@@ -71,7 +74,7 @@ parity tests' checker) on the host cores for a bounded sample of the same
 workload; the prefill field carries one of its own.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--only decode|decode06|prefill|long|store|mixed|linear|metadata|lm_head|all]
+                    [--only decode|decode06|prefill|long|store|mixed|linear|metadata|lm_head|host|all]
                     [--no-cpu-baseline]
                     [--copy-probe]
 """
@@ -113,7 +116,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", default="all",
                     choices=["decode", "decode06", "prefill", "long", "store", "mixed", "linear", "metadata", "lm_head",
-                             "all"])
+                             "host", "all"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 1 GiB device copy (counter scale for rocprofv3 --pmc)")
@@ -334,6 +337,74 @@ def bench_fp8_linear(M, N, K, steps, warmup, n_weights=2):
                 weight_gbs=weight_bytes / (ms_gemm * 1e-3) / 1e9,
                 quant_us=ms_quant * 1e3, quant_gbs=3.0 * M * K / (ms_quant * 1e-3) / 1e9,
                 linear_us=ms_linear * 1e3, flops=flops, weight_bytes=weight_bytes)
+
+
+def bench_host_overhead(calls=300):
+    """Host time per call of the drop-in Python entry points at the bench's
+    Qwen3-8B head shapes: wall-clock time of `calls` back-to-back calls with
+    nothing synchronised inside the loop (argument checks, workspace lookup,
+    ctypes, kernel launches), beside the decode launch through the C ABI with
+    its arguments prepared once (ctypes and launches only).  The inputs have
+    the shapes of the bench's workloads but short contexts, so that the GPU
+    keeps up and no launch waits for queue space: the host work does not
+    depend on the KV bytes."""
+    from nanovllm_amd import _native
+    from nanovllm_amd.kernels.fp8_linear import fp8_block_linear
+    lib = _native.load()
+    g = torch.Generator(device="cuda").manual_seed(7)
+    B, hq, hkv, bs, nb_pool, max_nb = 192, 32, 8, 256, 64, 16
+
+    def fp8(shape):
+        c = torch.randint(0, 120, shape, device="cuda", generator=g, dtype=torch.int32).to(torch.uint8)
+        return c.view(torch.float8_e4m3fn)
+
+    kc, vc = fp8((nb_pool, bs, hkv, 128)), fp8((nb_pool, bs, hkv, 128))
+    q = torch.randn(B, hq, 128, device="cuda", generator=g).to(torch.bfloat16)
+    bt = torch.randint(0, nb_pool, (B, max_nb), device="cuda", generator=g, dtype=torch.int32)
+    ctx = torch.randint(1, 64, (B,), device="cuda", generator=g, dtype=torch.int32)
+
+    def host_us(fn):
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            fn()
+        t1 = time.perf_counter()
+        torch.cuda.synchronize()
+        return round((t1 - t0) / calls * 1e6, 2)
+
+    res = dict(unit="us per call (host)", calls=calls)
+    res["fp8_decode_attention"] = host_us(lambda: fp8_decode_attention(q, kc, vc, bt, ctx, SCALE))
+    ws_n = lib.nvamd_decode_workspace_bytes(B, hq, hkv, max_nb, bs, 0)
+    ws = torch.empty(max(ws_n, 1), dtype=torch.uint8, device="cuda")
+    out = torch.empty_like(q)
+    args = (out.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), bt.data_ptr(), ctx.data_ptr(), B, hq, hkv, 128,
+            nb_pool, bs, max_nb, SCALE, 0, ws.data_ptr(), ws_n, torch.cuda.current_stream().cuda_stream)
+    dec = lib.nvamd_fp8_decode_attention
+    res["c_abi_decode"] = host_us(lambda: dec(*args))
+    # the mixed batch's varlen call: 32 speculative sequences of 5 rows + 3 chunks (64 rows here)
+    lq = [5] * 32 + [64] * 3
+    lk = [l + 40 for l in lq]
+    cu_q = torch.tensor([0] + list(np.cumsum(lq)), dtype=torch.int32, device="cuda")
+    cu_k = torch.tensor([0] + list(np.cumsum(lk)), dtype=torch.int32, device="cuda")
+    qv = torch.randn(int(sum(lq)), hq, 128, device="cuda", generator=g).to(torch.bfloat16)
+    btv = bt[:len(lq)].contiguous()
+    res["fp8_prefill_attention"] = host_us(lambda: fp8_prefill_attention(
+        qv, kc, vc, block_tables=btv, cu_seqlens_q=cu_q, cu_seqlens_k=cu_k, max_seqlen_q=max(lq),
+        max_seqlen_k=max(lk), softmax_scale=SCALE))
+    # the prefill step's 8192 new tokens, strided K/V views of a fused qkv tensor
+    qkv = torch.randn(8192, (hq + 2 * hkv) * 128, device="cuda", generator=g).to(torch.bfloat16)
+    key = qkv[:, hq * 128:(hq + hkv) * 128].view(8192, hkv, 128)
+    value = qkv[:, (hq + hkv) * 128:].view(8192, hkv, 128)
+    slots = torch.randperm(nb_pool * bs, device="cuda", generator=g)[:8192].to(torch.int32)
+    res["store_kvcache"] = host_us(lambda: store_kvcache(key, value, kc, vc, slots))
+    # the gate/up projection of 192 decode rows
+    x = torch.randn(B, 4096, device="cuda", generator=g).to(torch.bfloat16)
+    w = fp8((24576, 4096))
+    w_scale = (torch.rand(24576 // 128, 4096 // 128, device="cuda", generator=g) * 1e-3).to(torch.bfloat16)
+    res["fp8_block_linear"] = host_us(lambda: fp8_block_linear(x, w, w_scale))
+    return res
 
 
 def cpu_baseline_fp8_linear(N, K, rows=16, target_s=8.0):
@@ -793,6 +864,15 @@ def main():
             select_rows=dict(ms_per_step=round(sel["ms"], 5), rows=sel["rows"]))
         if not args.no_cpu_baseline:
             extra["lm_head"]["cpu_baseline"] = cpu_baseline_sampler(151936)
+        torch.cuda.empty_cache()
+
+    if args.only in ("host", "all"):
+        res = bench_host_overhead()
+        log("host time per call: " + ", ".join(f"{k} {v} us" for k, v in res.items() if isinstance(v, float)))
+        extra["host_overhead"] = dict(
+            workload="host time per call of the Python entry points (Qwen3-8B head shapes: 192-row decode, the "
+                     "mixed batch's 35-sequence varlen call, 8192-token store, 192 x 4096 -> 24576 FP8 linear)",
+            **res)
         torch.cuda.empty_cache()
 
     if "value" not in line:   # partial runs (profiling) still print one line
