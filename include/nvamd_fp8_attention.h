@@ -95,7 +95,8 @@ int32_t nvamd_store_kvcache(const void* key, int64_t key_stride0,
  * k_out: bf16 [num_tokens, num_kv_heads, head_dim] = RoPE(RMSNorm(k)), or NULL.
  * k_cache / v_cache, slot_mapping, num_slots: as nvamd_store_kvcache; the
  *   cache receives E4M3FN(RoPE(RMSNorm(k))) and E4M3FN(v).
- * head_dim must be 128; tensors 16-byte aligned (caches 8).
+ * head_dim must be 128; num_heads + 2 * num_kv_heads at most 128; tensors
+ * 16-byte aligned (caches 8).
  */
 int32_t nvamd_qk_norm_rope_store(const void* qkv, int64_t qkv_stride0, const int64_t* positions,
                                  const void* q_norm_weight, const void* k_norm_weight, float eps,

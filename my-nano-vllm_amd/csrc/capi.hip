@@ -241,6 +241,9 @@ int32_t nvamd_qk_norm_rope_store(const void* qkv, int64_t qkv_stride0, const int
                 (long long)num_tokens, num_heads, num_kv_heads, (long long)num_slots, (long long)max_position);
   if (!(eps >= 0.f) || !std::isfinite(eps))
     return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: eps must be finite and non-negative", fn);
+  if (num_heads + 2 * num_kv_heads > 128)
+    return fail(NVAMD_ERR_UNSUPPORTED, "%s: at most 128 head rows per token (num_heads + 2 * num_kv_heads = %d)", fn,
+                num_heads + 2 * num_kv_heads);
   if (qkv_stride0 < (int64_t)(num_heads + 2 * num_kv_heads) * head_dim)
     return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: qkv row stride %lld is shorter than a row", fn, (long long)qkv_stride0);
   if (num_tokens == 0) return ok();

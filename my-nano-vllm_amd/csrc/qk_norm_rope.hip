@@ -13,7 +13,8 @@
 // Layout: the projection output is [N, (Hq + 2 Hkv) * 128] bf16 with row
 // stride qkv_stride elements; a 16-lane group owns one 128-dim head row
 // (lane j: dims 8j .. 8j + 7, one 16-byte load), so a wave covers 4 head
-// rows and every access is a whole 16-byte granule of contiguous rows.
+// rows of one token and every access is a whole 16-byte granule of
+// contiguous rows.
 //
 // Arithmetic, with the reference's rounding points:
 //   RMSNorm:  y = bf16(x * rsqrt(mean(x^2) + eps)) in fp32, then
@@ -63,81 +64,92 @@ __device__ __forceinline__ u32x4 shfl_xor_u32x4(u32x4 w, int mask) {
 
 }  // namespace
 
+// One workgroup per token: 16-lane group g takes head rows g, g + 16, g + 32,
+// ... of the token, so the token's position and slot are uniform scalar
+// loads, no lane divides, and the cos / sin of the position and both norm
+// weights are loaded once per lane for all of its rows (they are reused
+// from the caches, but each load instruction costs address-unit time).
+constexpr int kRowsPerPass = 256 / kLanesPerRow;  // 16 head rows per pass of the workgroup
+constexpr int kMaxPasses = 8;                      // rows of a token: at most 128 (checked at launch)
+
 __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(QkNormRopeParams p) {
   const int rows_per_token = p.Hq + 2 * p.Hkv;
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t row = gid / kLanesPerRow;  // head row over all tokens
-  const int j = (int)(gid % kLanesPerRow);
-  // every lane of a 16-lane group stays until the cross-lane exchange: the
-  // groups of a wave are whole, and the grid covers whole rows
-  const bool live = row < p.num_tokens * rows_per_token;
-  const int64_t tok = live ? row / rows_per_token : 0;
-  const int r = live ? (int)(row - tok * rows_per_token) : 0;
-  const int32_t slot = live ? p.slot_mapping[tok] : -1;
+  const int64_t tok = blockIdx.x;
+  const int g = (int)(threadIdx.x >> 4);
+  const int j = (int)(threadIdx.x & 15);
+  const int32_t slot = p.slot_mapping[tok];
   const bool store = slot >= 0 && (int64_t)slot < p.num_slots;
   const int64_t cache_row = (int64_t)slot * p.Hkv * kHeadDim;
-
-  float x[8];
-  unpack8_bf16(live ? *reinterpret_cast<const u32x4*>(p.qkv + tok * p.qkv_stride + (int64_t)r * kHeadDim + 8 * j)
-                    : u32x4{0u, 0u, 0u, 0u},
-               x);
-  if (r >= p.Hq + p.Hkv) {  // v: stored as projected
-    if (live && store)
-      *reinterpret_cast<u32x2*>(p.v_cache + cache_row + (int64_t)(r - p.Hq - p.Hkv) * kHeadDim + 8 * j) = to_fp8x8(x);
-    return;  // whole groups take this branch: a row is q, k or v for all its lanes
-  }
-  const bool is_q = r < p.Hq;
-
-  // RMSNorm over the row's 128 dims (the 16 lanes of the group)
-  float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(x[i], x[i], ss);
-#pragma unroll
-  for (int m = 1; m < kLanesPerRow; m <<= 1) ss += shfl_xor_f32(ss, m);
-  const float rs = __builtin_amdgcn_rsqf(ss * (1.0f / kHeadDim) + p.eps);
-  float w[8];
-  unpack8_bf16(*reinterpret_cast<const u32x4*>((is_q ? p.q_weight : p.k_weight) + 8 * j), w);
-  float z[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float y = bf16_bits_to_f32(pack_bf16x2(x[i] * rs, 0.f) & 0xFFFFu);
-    z[i] = bf16_bits_to_f32(pack_bf16x2(y * w[i], 0.f) & 0xFFFFu);
-  }
-
-  // RoPE: lanes j and j ^ 8 hold dims i and i + 64 of the same frequencies
-  const u32x4 zp = pack8_bf16(z);  // exact: z is bf16
-  float other[8];
-  unpack8_bf16(shfl_xor_u32x4(zp, 8), other);
-  int64_t pos = live ? p.positions[tok] : 0;
+  int64_t pos = p.positions[tok];
   pos = pos < 0 ? 0 : (pos >= p.max_position ? p.max_position - 1 : pos);  // no read outside the table
+  const uint16_t* xrow = p.qkv + tok * p.qkv_stride + 8 * j;
+
+  // this lane's rows: all loads first
+  u32x4 xr[kMaxPasses];
+#pragma unroll
+  for (int i = 0; i < kMaxPasses; ++i) {
+    const int r = g + kRowsPerPass * i;
+    xr[i] = r < rows_per_token ? *reinterpret_cast<const u32x4*>(xrow + (int64_t)r * kHeadDim) : u32x4{0u, 0u, 0u, 0u};
+  }
+  // lanes j and j ^ 8 hold dims i and i + 64 of the same frequencies
   const float* cs = p.cos_sin + pos * kHeadDim + 8 * (j & 7);
   const f32x4 c0 = *reinterpret_cast<const f32x4*>(cs), c1 = *reinterpret_cast<const f32x4*>(cs + 4);
   const f32x4 s0 = *reinterpret_cast<const f32x4*>(cs + kHeadDim / 2);
   const f32x4 s1 = *reinterpret_cast<const f32x4*>(cs + kHeadDim / 2 + 4);
   const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
   const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+  float wq[8], wk[8];
+  unpack8_bf16(*reinterpret_cast<const u32x4*>(p.q_weight + 8 * j), wq);
+  unpack8_bf16(*reinterpret_cast<const u32x4*>(p.k_weight + 8 * j), wk);
   const float sgn = (j < 8) ? -1.f : 1.f;  // first half: z cos - other sin; second: z cos + other sin
-  float o[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) o[i] = bf16_bits_to_f32(pack_bf16x2(z[i] * cv[i] + sgn * (other[i] * sv[i]), 0.f) & 0xFFFFu);
-  if (!live) return;
 
-  const u32x4 out = pack8_bf16(o);
-  if (is_q) {
-    *reinterpret_cast<u32x4*>(p.q_out + (tok * p.Hq + r) * kHeadDim + 8 * j) = out;
-    return;
+#pragma unroll
+  for (int i = 0; i < kMaxPasses; ++i) {
+    const int r = g + kRowsPerPass * i;  // uniform in a 16-lane group, so the exchanges below stay in live lanes
+    if (r >= rows_per_token) break;
+    float x[8];
+    unpack8_bf16(xr[i], x);
+    if (r >= p.Hq + p.Hkv) {  // v: stored as projected
+      if (store) *reinterpret_cast<u32x2*>(p.v_cache + cache_row + (int64_t)(r - p.Hq - p.Hkv) * kHeadDim + 8 * j) = to_fp8x8(x);
+      continue;
+    }
+    const bool is_q = r < p.Hq;
+    // RMSNorm over the row's 128 dims (the 16 lanes of the group)
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(x[e], x[e], ss);
+#pragma unroll
+    for (int m = 1; m < kLanesPerRow; m <<= 1) ss += shfl_xor_f32(ss, m);
+    const float rs = __builtin_amdgcn_rsqf(ss * (1.0f / kHeadDim) + p.eps);
+    float z[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float y = bf16_bits_to_f32(pack_bf16x2(x[e] * rs, 0.f) & 0xFFFFu);
+      z[e] = bf16_bits_to_f32(pack_bf16x2(y * (is_q ? wq[e] : wk[e]), 0.f) & 0xFFFFu);
+    }
+    // RoPE
+    const u32x4 zp = pack8_bf16(z);  // exact: z is bf16
+    float other[8];
+    unpack8_bf16(shfl_xor_u32x4(zp, 8), other);
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      o[e] = bf16_bits_to_f32(pack_bf16x2(z[e] * cv[e] + sgn * (other[e] * sv[e]), 0.f) & 0xFFFFu);
+    const u32x4 out = pack8_bf16(o);
+    if (is_q) {
+      *reinterpret_cast<u32x4*>(p.q_out + (tok * p.Hq + r) * kHeadDim + 8 * j) = out;
+      continue;
+    }
+    const int hk = r - p.Hq;
+    if (p.k_out != nullptr) *reinterpret_cast<u32x4*>(p.k_out + (tok * p.Hkv + hk) * kHeadDim + 8 * j) = out;
+    if (store) *reinterpret_cast<u32x2*>(p.k_cache + cache_row + (int64_t)hk * kHeadDim + 8 * j) = to_fp8x8(o);
   }
-  const int hk = r - p.Hq;
-  if (p.k_out != nullptr) *reinterpret_cast<u32x4*>(p.k_out + (tok * p.Hkv + hk) * kHeadDim + 8 * j) = out;
-  if (store) *reinterpret_cast<u32x2*>(p.k_cache + cache_row + (int64_t)hk * kHeadDim + 8 * j) = to_fp8x8(o);
 }
 
 hipError_t launch_qk_norm_rope_store(const QkNormRopeParams& p, hipStream_t stream) {
   if (p.num_tokens == 0) return hipSuccess;
-  const int64_t threads = p.num_tokens * (p.Hq + 2 * p.Hkv) * kLanesPerRow;
-  const int64_t blocks = (threads + 255) / 256;
-  if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(qk_norm_rope_store_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, p);
+  if (p.num_tokens > 0x7fffffff || p.Hq + 2 * p.Hkv > kRowsPerPass * kMaxPasses) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(qk_norm_rope_store_kernel, dim3((unsigned)p.num_tokens), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -69,6 +69,17 @@ def test_rejects_partition_wider_than_the_block_table_window():
     assert nb > 0  # 1M-token capacity must be split
 
 
+def test_qk_norm_rope_store_rejects_more_than_128_head_rows_without_gpu():
+    """One workgroup per token takes at most 128 head rows (q + k + v)."""
+    lib = _native.load()
+    args = lambda hq, hkv: (None, (hq + 2 * hkv) * 128, None, None, None, 1e-6, None, 4096, None, None, None, None,
+                            None, 1, hq, hkv, 128, 16, None)
+    assert lib.nvamd_qk_norm_rope_store(*args(112, 16)) == 2
+    assert b"128 head rows" in lib.nvamd_last_error()
+    assert lib.nvamd_qk_norm_rope_store(*args(96, 16)) == 1   # 128 rows pass the shape checks (then: null pointers)
+    assert b"null pointer" in lib.nvamd_last_error()
+
+
 def test_fp8_linear_rejects_bad_shapes_without_gpu():
     """K and N must be multiples of the 128 block (fp8_linear.py:114)."""
     lib = _native.load()

@@ -78,9 +78,9 @@ def test_qwen3_8b_prefill_tokens():
     _check(res, 32, 8, slots, "qwen3-8b prefill tokens")
 
 
-@pytest.mark.parametrize("n,hq,hkv", [(1, 32, 8), (3, 4, 1), (37, 24, 8), (100, 64, 8), (9, 16, 2)])
+@pytest.mark.parametrize("n,hq,hkv", [(1, 32, 8), (3, 4, 1), (37, 24, 8), (100, 64, 8), (9, 16, 2), (5, 96, 16)])
 def test_ragged_shapes_padding_slots_and_strided_rows(n, hq, hkv):
-    """Odd token counts (partial workgroups), several GQA ratios, slot -1 rows
+    """Odd token counts, several GQA ratios (up to 128 head rows per token), slot -1 rows
     (no cache write), positions 0 and the last table row, and a projection
     output whose rows are longer than q + k + v (row stride > row)."""
     rng = np.random.default_rng(n * 100 + hq + hkv)
