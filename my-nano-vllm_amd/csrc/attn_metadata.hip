@@ -16,8 +16,10 @@
 // Input (device): `packed` = int32 [num_seqs, 4] descriptors {num_tokens,
 // num_cached_tokens, num_scheduled_tokens, table_len}, in that order, then the
 // sequences' block tables back to back (sum of table_len entries).  Every
-// workgroup loads the descriptors and scans them in LDS (token offsets, slot
-// offsets, output table rows, key-length prefix, table offsets), then walks
+// workgroup loads the descriptors into LDS once and scans them in one pass
+// (token offsets, slot offsets, output table rows, key-length prefix, table
+// offsets: per-thread chunk sums, a shuffle scan per wave, one exchange
+// between the waves), then walks
 // a grid-stride range of output units -- tokens, table entries, context
 // lengths, cu_seqlens entries -- locating each unit's sequence by binary
 // search.  Offsets are 64-bit; slot values are computed in 64 bits and
@@ -35,32 +37,6 @@ namespace {
 
 constexpr int kMetaThreads = 256;
 
-// Exclusive prefix over sequences of f(s) into out[0 .. n] (out[n] = total),
-// by per-thread chunks and a scan of the 256 chunk totals.
-template <typename F>
-__device__ void seq_scan(int n, int* out, int* tmp, F f) {
-  const int tid = threadIdx.x;
-  const int chunk = (n + kMetaThreads - 1) / kMetaThreads;
-  const int s0 = min(n, tid * chunk), s1 = min(n, s0 + chunk);
-  int local = 0;
-  for (int s = s0; s < s1; ++s) local += f(s);
-  tmp[tid] = local;
-  __syncthreads();
-  for (int off = 1; off < kMetaThreads; off <<= 1) {
-    const int v = tid >= off ? tmp[tid - off] : 0;
-    __syncthreads();
-    tmp[tid] += v;
-    __syncthreads();
-  }
-  int run = tmp[tid] - local;  // exclusive prefix of this thread's chunk
-  for (int s = s0; s < s1; ++s) {
-    out[s] = run;
-    run += f(s);
-  }
-  if (tid == kMetaThreads - 1) out[n] = tmp[tid];
-  __syncthreads();
-}
-
 // Last s in [0, n) with a[s] <= x (a nondecreasing, a[0] <= x).
 __device__ __forceinline__ int last_le(const int* a, int n, int64_t x) {
   int lo = 0, hi = n - 1;
@@ -73,27 +49,87 @@ __device__ __forceinline__ int last_le(const int* a, int n, int64_t x) {
 }
 
 __global__ __launch_bounds__(kMetaThreads) void build_metadata_kernel(AttnMetaParams p) {
+  __shared__ int4 dsc[kMetaMaxSeqs];          // the descriptors, negatives read as 0
   __shared__ int pos_off[kMetaMaxSeqs + 1];   // first token (query row) of each sequence
   __shared__ int slot_off[kMetaMaxSeqs + 1];  // first slot_mapping entry
   __shared__ int trow[kMetaMaxSeqs + 1];      // output block-table row (sequences with a table)
   __shared__ int kpre[kMetaMaxSeqs + 1];      // varlen key-length prefix (cu_seqlens_k)
   __shared__ int toff[kMetaMaxSeqs + 1];      // offset of the sequence's table in the upload
-  __shared__ int tmp[kMetaThreads];
+  __shared__ int wave_tot[kMetaThreads / 64][5];
   const int n = p.num_seqs, np_ = p.num_plain;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int4* desc = reinterpret_cast<const int4*>(p.packed);
   const int* tables = p.packed + 4 * (int64_t)n;
   const int64_t n_table_ints = p.packed_ints - 4 * (int64_t)n;  // table entries the upload holds
-  auto d = [&](int s) {  // {num_tokens, num_cached, num_scheduled, table_len}, negatives read as 0
-    const int4 v = desc[s];
-    return int4{max(v.x, 0), max(v.y, 0), max(v.z, 0), max(v.w, 0)};
-  };
+  for (int q = tid; q < n; q += kMetaThreads) {
+    const int4 v = desc[q];
+    dsc[q] = int4{max(v.x, 0), max(v.y, 0), max(v.z, 0), max(v.w, 0)};
+  }
+  __syncthreads();
+  auto d = [&](int q) { return dsc[q]; };  // {num_tokens, num_cached, num_scheduled, table_len}
   // table entry c of the table at offset o: -1 past the upload
   auto entry = [&](int64_t o, int64_t c) { return o + c < n_table_ints ? tables[o + c] : -1; };
-  seq_scan(n, pos_off, tmp, [&](int s) { return s < np_ ? 1 : d(s).z; });
-  seq_scan(n, slot_off, tmp, [&](int s) { return s < np_ ? 1 : (d(s).w > 0 ? d(s).z : 0); });
-  seq_scan(n, trow, tmp, [&](int s) { return d(s).w > 0 ? 1 : 0; });
-  seq_scan(n, kpre, tmp, [&](int s) { return s < np_ ? 0 : d(s).y + d(s).z; });
-  seq_scan(n, toff, tmp, [&](int s) { return d(s).w; });
+  // The five exclusive prefixes over the sequences in one pass: each thread
+  // sums a chunk of sequences, the chunk sums are scanned across the wave
+  // with shuffles and across the waves through LDS, then each thread writes
+  // its chunk's prefixes.
+  auto terms = [&](int q, int (&t)[5]) {
+    const int4 v = d(q);
+    const bool plain = q < np_;
+    t[0] = plain ? 1 : v.z;                          // query rows
+    t[1] = plain ? 1 : (v.w > 0 ? v.z : 0);          // slot_mapping entries
+    t[2] = v.w > 0 ? 1 : 0;                          // output table rows
+    t[3] = plain ? 0 : v.y + v.z;                    // varlen key lengths
+    t[4] = v.w;                                      // table entries in the upload
+  };
+  const int chunk = (n + kMetaThreads - 1) / kMetaThreads;
+  const int q0 = min(n, tid * chunk), q1 = min(n, q0 + chunk);
+  int sum[5] = {0, 0, 0, 0, 0};
+  for (int q = q0; q < q1; ++q) {
+    int t[5];
+    terms(q, t);
+#pragma unroll
+    for (int k = 0; k < 5; ++k) sum[k] += t[k];
+  }
+  int incl[5];
+#pragma unroll
+  for (int k = 0; k < 5; ++k) {
+    incl[k] = sum[k];
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int o = __shfl_up(incl[k], off, 64);
+      if (lane >= off) incl[k] += o;
+    }
+    if (lane == 63) wave_tot[wave][k] = incl[k];
+  }
+  __syncthreads();
+  int run[5], total[5];
+#pragma unroll
+  for (int k = 0; k < 5; ++k) {
+    int before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < kMetaThreads / 64; ++w) {
+      before += w < wave ? wave_tot[w][k] : 0;
+      all += wave_tot[w][k];
+    }
+    run[k] = before + incl[k] - sum[k];
+    total[k] = all;
+  }
+  int* const outs[5] = {pos_off, slot_off, trow, kpre, toff};
+  for (int q = q0; q < q1; ++q) {
+    int t[5];
+    terms(q, t);
+#pragma unroll
+    for (int k = 0; k < 5; ++k) {
+      outs[k][q] = run[k];
+      run[k] += t[k];
+    }
+  }
+  if (tid == 0) {
+#pragma unroll
+    for (int k = 0; k < 5; ++k) outs[k][n] = total[k];
+  }
+  __syncthreads();
 
   const int64_t T = pos_off[n], W = p.max_table_len, R = trow[n];
   const int n_var = n - np_;
@@ -145,8 +181,9 @@ __global__ __launch_bounds__(kMetaThreads) void build_metadata_kernel(AttnMetaPa
 hipError_t launch_build_metadata(const AttnMetaParams& p, int64_t units, hipStream_t stream) {
   if (p.num_seqs <= 0) return hipSuccess;
   if (p.num_seqs > kMetaMaxSeqs) return hipErrorInvalidValue;
-  // about 1,024 units per workgroup: each workgroup first scans all descriptors
-  const int64_t wgs = std::max<int64_t>(1, std::min<int64_t>(1024, (units + 1023) / 1024));
+  // one unit per lane (each unit is a chain of dependent loads); every
+  // workgroup first loads and scans all descriptors, which is short
+  const int64_t wgs = std::max<int64_t>(1, std::min<int64_t>(1024, (units + kMetaThreads - 1) / kMetaThreads));
   hipLaunchKernelGGL(build_metadata_kernel, dim3((unsigned)wgs), dim3(kMetaThreads), 0, stream, p);
   return hipGetLastError();
 }
