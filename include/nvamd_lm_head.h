@@ -64,7 +64,8 @@ int64_t nvamd_sample_workspace_bytes(int64_t rows);
  * mod 2^32, seed >> 32) that belongs to element v.  logits: [rows, vocab] of
  * logits_dtype (NVAMD_LOGITS_*), row stride stride0 elements; temperatures:
  * fp32 [rows], > 0; out: int64 [rows]; workspace: 16-byte aligned,
- * nvamd_sample_workspace_bytes(rows) bytes.
+ * nvamd_sample_workspace_bytes(rows) bytes.  vocab < 2^31 - 1
+ * (NVAMD_ERR_UNSUPPORTED beyond).
  */
 int32_t nvamd_sample(const void* logits, int32_t logits_dtype, int64_t stride0, int64_t rows, int64_t vocab,
                      const float* temperatures, const float* noise, uint64_t seed, uint64_t offset, int64_t* out,

@@ -422,10 +422,12 @@ int32_t nvamd_sample(const void* logits, int32_t logits_dtype, int64_t stride0, 
                      const float* temperatures, const float* noise, uint64_t seed, uint64_t offset, int64_t* out,
                      void* workspace, int64_t workspace_bytes, void* stream) {
   static const char* fn = "sample";
-  if (rows < 0 || rows > 0x7fffffff || vocab <= 0 || vocab > (1ll << 40) || stride0 < vocab ||
-      logits_dtype < NVAMD_LOGITS_BF16 || logits_dtype > NVAMD_LOGITS_F32)
+  if (rows < 0 || rows > 0x7fffffff || vocab <= 0 || stride0 < vocab || logits_dtype < NVAMD_LOGITS_BF16 ||
+      logits_dtype > NVAMD_LOGITS_F32)
     return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: bad sizes or dtype (rows=%lld vocab=%lld dtype=%d)", fn,
                 (long long)rows, (long long)vocab, logits_dtype);
+  if (vocab >= 0x7fffffff)
+    return fail(NVAMD_ERR_UNSUPPORTED, "%s: vocabulary of %lld entries: at most 2^31 - 2", fn, (long long)vocab);
   if (rows == 0) return ok();
   if (!logits || !temperatures || !out) return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
   const int parts = sample_parts(rows);

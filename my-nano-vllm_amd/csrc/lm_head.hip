@@ -92,54 +92,73 @@ __device__ __forceinline__ float load1(const void* row, int64_t v) {
 // score_v = z_v * log2(e) / T - log2(max(E_v, 1e-10)); the row's argmax of
 // score equals the reference's argmax of softmax(z / T)_v / max(E_v, 1e-10)
 // (the softmax's max and sum are the same for every v, and exp and log are
-// increasing), so one sweep of the logits suffices.
+// increasing), so one sweep of the logits suffices.  A lane visits its
+// elements in increasing index order, so a strict > keeps the first index
+// of a tie; the index order decides ties only across lanes and parts.
+// Indices are 32-bit (vocab < 2^31, checked at launch).
 template <int DT, bool VEC>
 __global__ __launch_bounds__(kSampleThreads) void sample_part_kernel(
-    const void* __restrict__ logits, int64_t stride, int64_t vocab, const float* __restrict__ temperatures,
+    const void* __restrict__ logits, int64_t stride, int64_t vocab64, const float* __restrict__ temperatures,
     const float* __restrict__ noise, uint64_t seed, uint64_t offset, int parts, float* __restrict__ part_score,
     int64_t* __restrict__ part_index) {
   __shared__ float bval[kSampleThreads / 64];
-  __shared__ int64_t bidx[kSampleThreads / 64];
+  __shared__ int bidx[kSampleThreads / 64];
+  const int vocab = (int)vocab64;
   const int64_t row = blockIdx.x / parts;
   const int part = (int)(blockIdx.x - row * parts);
   const int tid = threadIdx.x;
   const void* lr = static_cast<const uint8_t*>(logits) + row * stride * (DT == 2 ? 4 : 2);
+  const float* nr = noise != nullptr ? noise + row * vocab64 : nullptr;
   const float c1 = 1.4426950408889634f / temperatures[row];
-  const int64_t nb = (vocab + 3) / 4;
-  const int64_t j0 = nb * part / parts, j1 = nb * (part + 1) / parts;
+  const int nb = (vocab + 3) / 4, nb_full = vocab / 4;  // Philox blocks; those with 4 elements in the row
+  const int j0 = (int)((int64_t)nb * part / parts), j1 = (int)((int64_t)nb * (part + 1) / parts);
   const uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+  const uint32_t off_lo = (uint32_t)offset, off_hi = (uint32_t)(offset >> 32);
   float bv = -INFINITY;
-  int64_t bi = vocab;
-  for (int64_t j = j0 + tid; j < j1; j += kSampleThreads) {
-    const int64_t v0 = 4 * j;
+  int bi = vocab;
+  for (int j = j0 + tid; j < j1; j += kSampleThreads) {
+    const int v0 = 4 * j;
+    const bool full = j < nb_full;
     float z[4];
-    if (VEC && v0 + 4 <= vocab) {
+    if (VEC && full) {
       load4<DT>(lr, v0, z);
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i) z[i] = v0 + i < vocab ? load1<DT>(lr, v0 + i) : -INFINITY;
     }
     float e[4];
-    if (noise != nullptr) {
+    if (nr != nullptr) {
+      if (full) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) e[i] = v0 + i < vocab ? noise[row * vocab + v0 + i] : 1.f;
+        for (int i = 0; i < 4; ++i) e[i] = nr[v0 + i];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) e[i] = v0 + i < vocab ? nr[v0 + i] : 1.f;
+      }
     } else {
-      const u32x4 x = philox4x32_10(u32x4{(uint32_t)j, (uint32_t)row, (uint32_t)offset, (uint32_t)(offset >> 32)}, k0, k1);
+      const u32x4 x = philox4x32_10(u32x4{(uint32_t)j, (uint32_t)row, off_lo, off_hi}, k0, k1);
       const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i)  // E = -ln(u) = -log2(u) ln 2
         e[i] = -__builtin_amdgcn_logf((float)((xs[i] >> 8) + 1u) * 0x1p-24f) * 0.6931471805599453f;
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (v0 + i < vocab) better(bv, bi, z[i] * c1 - __builtin_amdgcn_logf(fmaxf(e[i], 1e-10f)), v0 + i);
+    for (int i = 0; i < 4; ++i) {  // past the row: z = -inf, never above bv
+      const float sc = z[i] * c1 - __builtin_amdgcn_logf(fmaxf(e[i], 1e-10f));
+      const bool up = sc > bv;
+      bv = up ? sc : bv;
+      bi = up ? v0 + i : bi;
+    }
   }
+  // (value, index): larger value wins, the smaller index on equal values
+  auto better32 = [](float& v, int& i, float ov, int oi) {
+    if (ov > v || (ov == v && oi < i)) {
+      v = ov;
+      i = oi;
+    }
+  };
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(bv, o, 64);
-    const int64_t oi = __shfl_xor(bi, o, 64);
-    better(bv, bi, ov, oi);
-  }
+  for (int o = 32; o > 0; o >>= 1) better32(bv, bi, __shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64));
   const int w = tid >> 6;
   if ((tid & 63) == 0) {
     bval[w] = bv;
@@ -147,7 +166,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_part_kernel(
   }
   __syncthreads();
   if (tid == 0) {
-    for (int i = 1; i < kSampleThreads / 64; ++i) better(bv, bi, bval[i], bidx[i]);
+    for (int i = 1; i < kSampleThreads / 64; ++i) better32(bv, bi, bval[i], bidx[i]);
     part_score[blockIdx.x] = bv;
     part_index[blockIdx.x] = bi;
   }
@@ -183,7 +202,7 @@ hipError_t launch_sample(const void* logits, int dtype, int64_t stride, int64_t 
                          const float* temperatures, const float* noise, uint64_t seed, uint64_t offset, int64_t* out,
                          float* part_score, int64_t* part_index, int parts, hipStream_t stream) {
   if (rows == 0) return hipSuccess;
-  if (parts < 1 || rows * parts > 0x7fffffff) return hipErrorInvalidValue;
+  if (parts < 1 || rows * parts > 0x7fffffff || vocab >= 0x7fffffff) return hipErrorInvalidValue;
   const dim3 grid((unsigned)(rows * parts)), block(kSampleThreads);
   // vector loads need every row start aligned to 4 elements
   const bool vec = (stride % 4 == 0) && ((uintptr_t)logits % (dtype == 2 ? 16 : 8) == 0);
