@@ -286,6 +286,9 @@ int32_t nvamd_fp8_act_quant(const void* x, int64_t x_stride0, int32_t x_dtype, v
   if (x_dtype != NVAMD_DTYPE_BF16 && x_dtype != NVAMD_DTYPE_F16)
     return fail(NVAMD_ERR_UNSUPPORTED, "%s: x_dtype must be bf16 or fp16 (got %d)", fn, x_dtype);
   if (M == 0) return ok();
+  if (M > 0x7fffffffll || K > 128ll * 16 * 0xffff)
+    return fail(NVAMD_ERR_UNSUPPORTED, "%s: M=%lld K=%lld beyond the launch grid (M < 2^31, K < 2^27)", fn,
+                (long long)M, (long long)K);
   if (!x || !xq || !x_scale) return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
   if ((uintptr_t)x % 16 != 0 || x_stride0 % 8 != 0 || (uintptr_t)xq % 8 != 0 || (uintptr_t)x_scale % 2 != 0)
     return fail(NVAMD_ERR_UNSUPPORTED, "%s: x must be 16-byte aligned with a row stride of 8 elements (xq 8-byte aligned)",

@@ -5,8 +5,9 @@
 //   act_quant_kernel   <- fp8_dyn_quant_kernel  (fp8_linear.py:11-31, launched at :116-123)
 //   block_gemm_kernel  <- fp8_block_gemm_kernel (fp8_linear.py:34-71, launched at :125-138)
 //
-// Quantisation: one 16-lane group per (token m, 128-column group g); lane j
-// loads 8 consecutive values (one 16-byte load).  amax over the group by
+// Quantisation: one 16-lane group per (token m, 128-column group g), the
+// token from the workgroup's index; lane j loads 8 consecutive values (one
+// 16-byte load).  amax over the group by
 // cross-lane exchange; scale = amax / 448 (IEEE fp32 division), 1 when not
 // > 0; xq = E4M3FN(clamp(x / scale)) (IEEE division, RNE); the scale is stored
 // as bf16 (RNE), x_scale[m, g].  Purely HBM-bound: 2 B read + 1 B written per
@@ -56,18 +57,17 @@ __device__ __forceinline__ float in_to_f32(uint32_t bits16) {
   return bf16_bits_to_f32(bits16);
 }
 
+// Grid (M, ceil(Kc / 16)): workgroup (m, y) quantises groups 16 y .. 16 y + 15
+// of token m, one 16-lane group each, so no lane divides.
 template <bool F16_IN>
 __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restrict__ x, int64_t x_stride,
                                                         uint8_t* __restrict__ xq, uint16_t* __restrict__ x_scale,
                                                         int64_t M, int Kc) {
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t grp = gid >> 4;  // (token, group) index; whole 16-lane groups share it
-  const int j = (int)(gid & 15);
-  const bool live = grp < M * Kc;
-  const int64_t m = live ? grp / Kc : 0;
-  const int g = live ? (int)(grp - m * Kc) : 0;
-  u32x4 w = {0u, 0u, 0u, 0u};
-  if (live) w = *reinterpret_cast<const u32x4*>(x + m * x_stride + (int64_t)g * kFp8Block + 8 * j);
+  const int64_t m = blockIdx.x;
+  const int g = 16 * (int)blockIdx.y + (int)(threadIdx.x >> 4);  // 128-column group of the token
+  const int j = (int)(threadIdx.x & 15);
+  if (g >= Kc) return;  // whole 16-lane groups
+  const u32x4 w = *reinterpret_cast<const u32x4*>(x + m * x_stride + (int64_t)g * kFp8Block + 8 * j);
   const uint32_t d[4] = {w.x, w.y, w.z, w.w};
   float v[8];
 #pragma unroll
@@ -85,7 +85,6 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restri
   float y[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) y[i] = v[i] / scale;  // clamp and RNE in f32x4_to_fp8x4
-  if (!live) return;
   *reinterpret_cast<u32x2*>(xq + m * ((int64_t)Kc * kFp8Block) + (int64_t)g * kFp8Block + 8 * j) =
       u32x2{f32x4_to_fp8x4(y[0], y[1], y[2], y[3]), f32x4_to_fp8x4(y[4], y[5], y[6], y[7])};
   if (j == 0) x_scale[m * Kc + g] = (uint16_t)(pack_bf16x2(scale, 0.f) & 0xFFFFu);
@@ -302,15 +301,15 @@ hipError_t launch_config(const Fp8GemmParams& p, int64_t lds, hipStream_t stream
 hipError_t launch_fp8_act_quant(const void* x, int64_t x_stride, bool f16_in, void* xq, void* x_scale, int64_t M,
                                 int64_t K, hipStream_t stream) {
   if (M == 0) return hipSuccess;
-  const int64_t threads = M * (K / kFp8Block) * 16;
-  const int64_t blocks = (threads + 255) / 256;
-  if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+  const int64_t ys = (K / kFp8Block + 15) / 16;
+  if (M > 0x7fffffff || ys > 0xffff) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)M, (unsigned)ys);
   if (f16_in)
-    hipLaunchKernelGGL(act_quant_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream, (const uint16_t*)x,
-                       x_stride, (uint8_t*)xq, (uint16_t*)x_scale, M, (int)(K / kFp8Block));
+    hipLaunchKernelGGL(act_quant_kernel<true>, grid, dim3(256), 0, stream, (const uint16_t*)x, x_stride, (uint8_t*)xq,
+                       (uint16_t*)x_scale, M, (int)(K / kFp8Block));
   else
-    hipLaunchKernelGGL(act_quant_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream, (const uint16_t*)x,
-                       x_stride, (uint8_t*)xq, (uint16_t*)x_scale, M, (int)(K / kFp8Block));
+    hipLaunchKernelGGL(act_quant_kernel<false>, grid, dim3(256), 0, stream, (const uint16_t*)x, x_stride,
+                       (uint8_t*)xq, (uint16_t*)x_scale, M, (int)(K / kFp8Block));
   return hipGetLastError();
 }
 
