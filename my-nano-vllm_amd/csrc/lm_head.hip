@@ -30,21 +30,21 @@ namespace {
 
 constexpr int kSampleThreads = 512;
 
+// Workgroup r copies output row r: its source row from the prefix rule
+// (uniform scalar loads), then the row's 16-byte chunks, strided over the
+// 256 lanes.
 __global__ __launch_bounds__(256) void select_rows_kernel(const uint8_t* __restrict__ x, int64_t x_stride_bytes,
                                                           int64_t x_rows, int row_bytes,
                                                           const int32_t* __restrict__ cu_seqlens_q, int split_pt,
                                                           int num_spec_rows, int num_spec_seqs, int64_t out_rows,
                                                           uint8_t* __restrict__ out, int64_t out_stride_bytes) {
-  const int chunks = row_bytes / 16;
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t r = gid / chunks;
-  const int c = (int)(gid - r * chunks);
-  if (r >= out_rows) return;
+  const int64_t r = blockIdx.x;
   const int64_t prefix = (int64_t)split_pt + num_spec_rows;
   const int64_t src = r < prefix ? r : split_pt + (int64_t)cu_seqlens_q[num_spec_seqs + 1 + (r - prefix)] - 1;
   if (src < 0 || src >= x_rows) return;
-  *reinterpret_cast<u32x4*>(out + r * out_stride_bytes + 16 * c) =
-      *reinterpret_cast<const u32x4*>(x + src * x_stride_bytes + 16 * c);
+  const u32x4* in = reinterpret_cast<const u32x4*>(x + src * x_stride_bytes);
+  u32x4* o = reinterpret_cast<u32x4*>(out + r * out_stride_bytes);
+  for (int c = (int)threadIdx.x; c < row_bytes / 16; c += 256) o[c] = in[c];
 }
 
 // Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11).
@@ -189,10 +189,8 @@ hipError_t launch_select_rows(const void* x, int64_t x_stride_bytes, int64_t x_r
                               const int32_t* cu_seqlens_q, int split_pt, int num_spec_rows, int num_spec_seqs,
                               int64_t out_rows, void* out, int64_t out_stride_bytes, hipStream_t stream) {
   if (out_rows == 0) return hipSuccess;
-  const int64_t threads = out_rows * (row_bytes / 16);
-  const int64_t blocks = (threads + 255) / 256;
-  if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(select_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, (const uint8_t*)x,
+  if (out_rows > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(select_rows_kernel, dim3((unsigned)out_rows), dim3(256), 0, stream, (const uint8_t*)x,
                      x_stride_bytes, x_rows, row_bytes, cu_seqlens_q, split_pt, num_spec_rows, num_spec_seqs,
                      out_rows, (uint8_t*)out, out_stride_bytes);
   return hipGetLastError();
