@@ -226,3 +226,19 @@ def test_prefill_zero_length_sequences():
     wl = W.make_workload("prefill_zero_lq", 32, 8, seqs, seed=23)
     announce("prefill: zero-length sequences in the batch")
     _check(wl)
+
+
+@pytest.mark.parametrize("q_scale", [4096.0, 1.0e6])
+def test_prefill_large_queries(q_scale):
+    """The first sequence's queries scaled up.  At 4096 every q * scale * log2(e)
+    still fits fp16 (the scaled form, QK^T on fp16 operands) and the scores are
+    sharply peaked; at 10^6 some do not, and those workgroups keep q in bf16
+    and scale each score instead.  Both must match the oracle."""
+    seqs = [W.SeqSpec(lq=l, cached=c) for l, c in ((200, 300), (64, 0), (129, 1000))]
+    wl = W.make_workload("prefill_large_q", 32, 8, seqs, seed=25)
+    announce(f"prefill: queries of sequence 0 scaled by {q_scale:g}")
+    cpu_c, gpu_c = build_pair(wl)
+    q = wl.make_q("cpu")
+    q[:200] = (q[:200].float() * q_scale).to(torch.bfloat16)
+    out = _prefill_gpu(wl, gpu_c, q.cuda())
+    assert_close(out, _prefill_oracle(wl, cpu_c, q), f"{wl.name} x{q_scale:g}")
