@@ -704,10 +704,17 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
     }
     l_run = L;
   }
-  const int64_t row = (int64_t)q_start + tq;
-  if (tq < Lq && row < p.q_rows) {
+  // Output through LDS: a lane holds 4-dim pieces of its query row, so
+  // storing from registers writes 16 bytes into each of 32 rows 8 KiB apart
+  // per instruction.  Each wave writes its 32 x 128 bf16 rows to a region of
+  // its own (the tile buffers: every wave passed the last step's barrier, so
+  // no wave reads them any more), then stores whole rows: 16 lanes per row,
+  // 4 rows per instruction.  A wave reads back only what it wrote, and its
+  // LDS accesses complete in order, so no barrier is needed.
+  {
+    constexpr int kOPitch = kHeadDim + 8;  // bf16 per row in LDS (272 B)
+    uint16_t* ob = lds + wave * 32 * kOPitch;
     const float inv = (l_run > 0.f) ? 1.0f / l_run : 0.f;
-    uint16_t* op = p.out + (row * p.Hq + head) * kHeadDim;
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
 #pragma unroll
@@ -716,8 +723,18 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
         u32x2 w;
         w.x = out_round_bf16_bits(acc[db][4 * b4 + 0] * inv) | (out_round_bf16_bits(acc[db][4 * b4 + 1] * inv) << 16);
         w.y = out_round_bf16_bits(acc[db][4 * b4 + 2] * inv) | (out_round_bf16_bits(acc[db][4 * b4 + 3] * inv) << 16);
-        *reinterpret_cast<u32x2*>(op + d) = w;
+        *reinterpret_cast<u32x2*>(ob + col * kOPitch + d) = w;
       }
+    }
+    const int chunk = lane & 15;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int r = 4 * j + (lane >> 4);  // row of the wave's 32
+      const u32x4 v = *reinterpret_cast<const u32x4*>(ob + r * kOPitch + 8 * chunk);
+      const int tr = m0w + r;
+      const int64_t grow = (int64_t)q_start + tr;
+      if (tr < Lq && grow < p.q_rows)
+        *reinterpret_cast<u32x4*>(p.out + (grow * p.Hq + head) * kHeadDim + 8 * chunk) = v;
     }
   }
 }
