@@ -62,6 +62,7 @@ constexpr int kVPitch = kBN + 8;              // fp16 per V^T row in LDS (144 B)
 constexpr int kKElems = kBN * kKPitch;        // 8704
 constexpr int kVElems = kHeadDim * kVPitch;   // 9216
 constexpr int kBufElems = kKElems + kVElems;  // 17920 16-bit = 35840 B per K + V pair
+constexpr int kQPitch = kHeadDim + 8;         // bf16 per Q row in a wave's LDS slice (272 B)
 constexpr int kBtWindow = 64;                 // block-table entries held in one register
 constexpr int kLead = 4;                      // MFMA operands are read from LDS this many MFMAs ahead
 // A tile's row sum of fp16 weights above this moves the reference maximum
@@ -159,8 +160,15 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
   const int m0w = m0 + 32 * tw;          // first query token of this wave
   const int tq = m0w + col;              // this lane's query token
 
-  // ---- Q operand (B of S^T): dims 16ks + 8h + [0,8); rows past the sequence
-  // (or past q) read as zero through a bounded buffer descriptor, no branches
+  // ---- Q operand (B of S^T): dims 16ks + 8h + [0,8) of query row col.
+  // Loaded whole rows at a time (16 lanes x 16 bytes per 256-byte row, 4 rows
+  // per instruction) into the wave's own LDS slice, then read back in the
+  // operand layout: loaded in that layout directly, each instruction would
+  // touch 32 rows 8 KiB apart for 32 bytes of each.  A wave reads back only
+  // what it wrote, and its LDS accesses complete in order, so no barrier is
+  // needed.  Rows past the sequence (or past q) read as zero through a
+  // bounded buffer descriptor, no branches.
+  __shared__ __attribute__((aligned(16))) uint16_t q_lds[kPrefillWaves * 32 * kQPitch];
   bf16x8 qop[8];
   {
     const int64_t row = (int64_t)q_start + m0w;
@@ -168,9 +176,16 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
     const uint32_t row_bytes = (uint32_t)(p.Hq * kHeadDim * 2);
     const __amdgpu_buffer_rsrc_t qr =
         make_rsrc(p.q + (row * p.Hq + head) * kHeadDim, rows == 0 ? 0u : (rows - 1) * row_bytes + kHeadDim * 2);
-    const uint32_t qoff = (uint32_t)col * row_bytes + 16 * h;
+    uint16_t* qs = q_lds + wave * 32 * kQPitch;
+    const int chunk = lane & 15, r0 = lane >> 4;
+    u32x4 qv[8];
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) qop[ks] = as_bf16x8(buf_load16(qr, qoff + 32 * ks));
+    for (int j = 0; j < 8; ++j) qv[j] = buf_load16(qr, (uint32_t)(4 * j + r0) * row_bytes + 16 * chunk);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x4*>(qs + (4 * j + r0) * kQPitch + 8 * chunk) = qv[j];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+      qop[ks] = as_bf16x8(*reinterpret_cast<const u32x4*>(qs + col * kQPitch + 16 * ks + 8 * h));
   }
 
   f32x16 acc[4];
