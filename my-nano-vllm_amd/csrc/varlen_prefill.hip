@@ -49,6 +49,7 @@
 
 #include "fp8_common.h"
 #include "kernels.h"
+#include "lds_dma.h"
 #include "mq_merge.h"
 #include "prefill_items.h"
 
@@ -62,7 +63,8 @@ constexpr int kVPitch = kBN + 8;              // fp16 per V^T row in LDS (144 B)
 constexpr int kKElems = kBN * kKPitch;        // 8704
 constexpr int kVElems = kHeadDim * kVPitch;   // 9216
 constexpr int kBufElems = kKElems + kVElems;  // 17920 16-bit = 35840 B per K + V pair
-constexpr int kQPitch = kHeadDim + 8;         // bf16 per Q row in a wave's LDS slice (272 B)
+constexpr int kQRowBytes = kHeadDim * 2;      // bytes per bf16 Q row (in a wave's LDS slice too)
+constexpr int kQSliceBytes = 32 * kQRowBytes + 256;  // a wave's 32 Q rows + 64 block-table entries
 constexpr int kBtWindow = 64;                 // block-table entries held in one register
 constexpr int kLead = 4;                      // MFMA operands are read from LDS this many MFMAs ahead
 // A tile's row sum of fp16 weights above this moves the reference maximum
@@ -162,31 +164,49 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
 
   // ---- Q operand (B of S^T): dims 16ks + 8h + [0,8) of query row col.
   // Loaded whole rows at a time (16 lanes x 16 bytes per 256-byte row, 4 rows
-  // per instruction) into the wave's own LDS slice, then read back in the
-  // operand layout: loaded in that layout directly, each instruction would
-  // touch 32 rows 8 KiB apart for 32 bytes of each.  A wave reads back only
-  // what it wrote, and its LDS accesses complete in order, so no barrier is
-  // needed.  Rows past the sequence (or past q) read as zero through a
-  // bounded buffer descriptor, no branches.
-  __shared__ __attribute__((aligned(16))) uint16_t q_lds[kPrefillWaves * 32 * kQPitch];
-  bf16x8 qop[8];
+  // per instruction) straight into the wave's own LDS slice, then read back
+  // in the operand layout: loaded in that layout directly, each instruction
+  // would touch 32 rows 8 KiB apart for 32 bytes of each.  Chunk c of row r
+  // sits in slot c ^ (r % 16) of the row, so the 16 lanes of an operand read
+  // hit 16 different slots.  A wave reads back only what it loaded.  Rows
+  // past the sequence (or past q) read as zero through a bounded buffer
+  // descriptor, no branches.
+  // The start of a workgroup is a chain of loads: the first block-table
+  // window's entries go out first (to LDS, beside the wave's Q rows), then
+  // Q; the tile loop waits for the window only (loads complete in order, so
+  // vmcnt(8) leaves the 8 Q loads in flight) and issues the first tile
+  // loads before it waits for Q, so Q's loads overlap both round trips.
+  // Both are direct-to-LDS loads, which the compiler's wait counts do not
+  // see: every wait for them is explicit.
+  const int win_tiles = PAGED ? kBtWindow * p.block_size / kBN : max(n_tiles, 1);
+  __shared__ __attribute__((aligned(16))) uint8_t q_lds[kPrefillWaves * kQSliceBytes];
+  const uint8_t* qs = q_lds + wave * kQSliceBytes;
+  const uint8_t* bt_first = qs + 32 * kQRowBytes;  // the first window's entries, one dword per lane
+  if constexpr (PAGED) {
+    const int bi = min(t_lo / win_tiles * kBtWindow + lane, (int)p.bt_stride - 1);
+    dma_load4_keep(rsrc_words(p.block_tables + (int64_t)seq * p.bt_stride, (uint32_t)p.bt_stride * 4u),
+                   (uint32_t)bi * 4u, lds_addr(bt_first));
+  }
   {
     const int64_t row = (int64_t)q_start + m0w;
     const uint32_t rows = (uint32_t)max<int64_t>(0, min<int64_t>(min(Lq - m0w, 32), p.q_rows - row));
     const uint32_t row_bytes = (uint32_t)(p.Hq * kHeadDim * 2);
-    const __amdgpu_buffer_rsrc_t qr =
-        make_rsrc(p.q + (row * p.Hq + head) * kHeadDim, rows == 0 ? 0u : (rows - 1) * row_bytes + kHeadDim * 2);
-    uint16_t* qs = q_lds + wave * 32 * kQPitch;
-    const int chunk = lane & 15, r0 = lane >> 4;
-    u32x4 qv[8];
+    const u32x4 qr =
+        rsrc_words(p.q + (row * p.Hq + head) * kHeadDim, rows == 0 ? 0u : (rows - 1) * row_bytes + kQRowBytes);
+    const int r0 = lane >> 4, slot = lane & 15;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) qv[j] = buf_load16(qr, (uint32_t)(4 * j + r0) * row_bytes + 16 * chunk);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x4*>(qs + (4 * j + r0) * kQPitch + 8 * chunk) = qv[j];
+    for (int j = 0; j < 8; ++j) {
+      const int r = 4 * j + r0;
+      dma_load16_keep(qr, (uint32_t)r * row_bytes + 16 * (slot ^ (r & 15)), lds_addr(qs + 4 * j * kQRowBytes));
+    }
+  }
+  bf16x8 qop[8];
+  auto q_to_operands = [&] {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the Q loads (and every later load) have landed
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks)
-      qop[ks] = as_bf16x8(*reinterpret_cast<const u32x4*>(qs + col * kQPitch + 16 * ks + 8 * h));
-  }
+      qop[ks] = as_bf16x8(*reinterpret_cast<const u32x4*>(qs + col * kQRowBytes + 16 * ((2 * ks + h) ^ (col & 15))));
+  };
 
   f32x16 acc[4];
 #pragma unroll
@@ -520,26 +540,42 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
   uint16_t* vbuf1 = vbuf0 + kVElems;
   // Window w holds the blocks of tiles [w * win_tiles, (w + 1) * win_tiles);
   // a piece starts inside one and ends inside one.
-  const int win_tiles = PAGED ? kBtWindow * p.block_size / kBN : max(n_tiles, 1);
   // The tile loop, specialised for the wave's role (K or V staging).
   auto tile_loop = [&](auto role) {
-  for (int t0 = t_lo, t1; t0 < n_tiles; t0 = t1) {
+  int t0 = t_lo, t1 = 0;
+  auto in_win = [&](int t) { return t < t1 ? t : n_tiles; };
+  TileRegs ra, rb;
+  // Start of t0's window: its block offsets, the first tiles loaded and
+  // staged, the next step's load issued.  The piece's first window is its
+  // own copy (kFirst), placed before the loop: there the only loads in
+  // flight are the direct-to-LDS block-table and Q loads, and the wait for
+  // the table entries leaves the Q loads in flight (inside the loop the
+  // compiler's waits would also cover loads of the previous window).
+  auto window_start = [&](auto first) {
+    constexpr bool kFirst = decltype(first)::value;
     const int win = t0 / win_tiles;
     t1 = min(n_tiles, (win + 1) * win_tiles);
     if constexpr (PAGED) {
       win_base = win * kBtWindow;
-      const int bi = min(win_base + lane, (int)p.bt_stride - 1);
-      const int blk = p.block_tables[(int64_t)seq * p.bt_stride + bi];
+      int blk;
+      if constexpr (kFirst) {
+        // the entries were loaded before the 8 Q loads
+        asm volatile("s_waitcnt vmcnt(8)\n\tds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)"
+                     : "=v"(blk)
+                     : "v"(lds_addr(bt_first) + 4u * (uint32_t)lane)
+                     : "memory");
+      } else {
+        blk = p.block_tables[(int64_t)seq * p.bt_stride + min(win_base + lane, (int)p.bt_stride - 1)];
+      }
       const int64_t row = (int64_t)blk * p.block_size;
       const int64_t off = (blk >= 0 && row + p.block_size <= p.kv_rows) ? (row * p.Hkv + g) * kHeadDim : -1;
       blk_lo = (uint32_t)off;
       blk_hi = (uint32_t)((uint64_t)off >> 32);
     }
-    auto in_win = [&](int t) { return t < t1 ? t : n_tiles; };
-    TileRegs ra, rb;
     load(role, t0, t0, ra);
+    if constexpr (decltype(role)::value) load(role, in_win(t0 + 1), 0, rb);
+    if constexpr (kFirst) q_to_operands();
     if constexpr (decltype(role)::value) {
-      load(role, in_win(t0 + 1), 0, rb);
       stage_k(ra, kbuf0);
       stage_k(rb, kbuf1);
     } else {
@@ -548,6 +584,13 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
     load(role, in_win(t0 + 2), in_win(t0 + 1), ra);
     wait_lds();
     __syncthreads();
+  };
+  if (t0 >= n_tiles) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no direct-to-LDS load outlives the wave
+    return;
+  }
+  window_start(std::true_type{});
+  for (;;) {
     // Prologue: S_{t0}, its maximum and the exponentials of its words 0..3.
     f32x16 sa[2], sb[2];
     uint32_t pa[16], pb[16];
@@ -616,6 +659,9 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
       idle_step(t, ra, kbuf0, vbuf1, rb);
       if (t + 1 < t1) idle_step(t + 1, rb, kbuf1, vbuf0, ra);
     }
+    t0 = t1;
+    if (t0 >= n_tiles) break;
+    window_start(std::false_type{});
   }
   };
   if (k_role) tile_loop(std::true_type{});
