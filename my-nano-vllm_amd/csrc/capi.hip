@@ -193,7 +193,7 @@ PrefillLayout prefill_layout(int32_t num_seqs, int32_t num_kv_heads, int g, int3
   L.slots_per_group = std::max<int64_t>(1, device_cu_count() / n_groups);
   L.records = std::max(n_items, 2 * L.slots_per_group);
   L.list_bytes = align_up(L.records * kPrefillItemBytes);
-  L.counter_bytes = align_up(L.slots_per_group * n_groups * (int64_t)sizeof(int));
+  L.counter_bytes = align_up((L.slots_per_group * n_groups + 3) * (int64_t)sizeof(int));
   L.part_bytes = 2 * L.slots_per_group * n_groups * nvamd::kPrefillPartDwords * 64 * nvamd::kPrefillWaves *
                  (int64_t)sizeof(uint32_t);
   return L;

@@ -74,7 +74,8 @@ struct PrefillParams {
   // pieces whose partial results the item's last piece merges.
   int n_records;        // work-list records: max(num_seqs * n_mblocks, 2 * slots_per_group)
   int slots_per_group;  // workgroups a kv-head group gets in one round: CUs / (Hkv * n_hgroups), >= 1
-  int* counters;        // [slots_per_group][Hkv * n_hgroups] arrivals per split item and group
+  int* counters;        // [slots_per_group][Hkv * n_hgroups] arrivals per split item and group, then the
+                        // last round's claim counter and {claim_from, total_units} (see prefill_schedule)
   uint32_t* part;       // [2 * slots_per_group][Hkv * n_hgroups][kPrefillPartDwords][64 * kPrefillWaves]
 };
 

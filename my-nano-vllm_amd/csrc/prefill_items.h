@@ -114,7 +114,7 @@ __device__ __forceinline__ void prefill_schedule(const PrefillParams& p, Prefill
   const int n_groups = p.Hkv * p.n_hgroups;
   if (worker) {
     for (int b = tid; b < kCostBuckets; b += 256) hist[b] = 0;
-    for (int c = tid; c < p.slots_per_group * n_groups; c += 256) p.counters[c] = 0;
+    for (int c = tid; c <= p.slots_per_group * n_groups; c += 256) p.counters[c] = 0;  // + the claim counter
   }
   // candidate idx: its geometry and tile count (-1: not a valid item)
   auto candidate = [&](int idx, ItemGeom& g) {
@@ -223,6 +223,15 @@ __device__ __forceinline__ void prefill_schedule(const PrefillParams& p, Prefill
   if (worker)
     for (int pos = total + tid; pos < p.n_records; pos += 256)
       items[pos] = PrefillItem{make_int4(-1, 0, 0, 0), make_int4(0, 0, 0, 0), make_int4(0, 1, -1, -1)};
+  // The last round of workgroups claims its units (record, group) in the
+  // order the workgroups start: a workgroup goes to XCD blockIdx % 8 however
+  // busy that XCD is, and the XCDs run at different rates, so the XCDs that
+  // reach the last round first take its longest units.
+  if (tid == 0) {
+    const int round = p.slots_per_group * n_groups, units = total * n_groups;
+    p.counters[round + 1] = units > round ? units - round : units;  // claim_from
+    p.counters[round + 2] = units;                                   // total_units
+  }
 }
 
 }  // namespace nvamd

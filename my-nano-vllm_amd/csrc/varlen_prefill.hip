@@ -136,12 +136,38 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
     return;
   }
 
-  // blockIdx.x = record * n_groups + group: the kv-head group varies fastest.
+  // Unit blockIdx.x = record * n_groups + group (the kv-head group varies
+  // fastest); the last round's workgroups claim theirs in the order they
+  // start (the schedule pass zeroed the counter and wrote the bounds).  The
+  // bounds are scalar loads beside the record's, so a workgroup that does not
+  // claim waits for neither longer than for its record.
   const int n_groups = p.Hkv * p.n_hgroups;
-  const int item = (int)(blockIdx.x / (unsigned)n_groups);
-  const int grp = (int)blockIdx.x - item * n_groups;
+  int unit = (int)blockIdx.x;
+  int item = (int)((unsigned)unit / (unsigned)n_groups);
   // one record load gives the piece and its geometry
-  const int4 rec_a = items[item].head, rec_b = items[item].tail, rec_c = items[item].split;
+  int4 rec_a = items[item].head, rec_b = items[item].tail, rec_c = items[item].split;
+  {
+    int* claim = p.counters + p.slots_per_group * n_groups;
+    const auto* bounds = (const __attribute__((address_space(4))) int*)(claim + 1);
+    const int claim_from = bounds[0], total_units = bounds[1];
+    // the bounds and the record are loaded together (the record is reloaded
+    // only by a workgroup that claims)
+    asm volatile("" ::"s"(claim_from), "s"(total_units), "s"(rec_a.x), "s"(rec_a.y), "s"(rec_a.z), "s"(rec_a.w),
+                 "s"(rec_b.x), "s"(rec_b.y), "s"(rec_b.z), "s"(rec_b.w), "s"(rec_c.x), "s"(rec_c.y), "s"(rec_c.z),
+                 "s"(rec_c.w));
+    if (unit >= claim_from && unit < total_units) {
+      __shared__ int s_unit;
+      if (threadIdx.x == 0)
+        s_unit = claim_from + __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __syncthreads();
+      unit = s_unit;
+      item = (int)((unsigned)unit / (unsigned)n_groups);
+      rec_a = items[item].head;
+      rec_b = items[item].tail;
+      rec_c = items[item].split;
+    }
+  }
+  const int grp = unit - item * n_groups;
   const int seq = wave_uniform(rec_a.x);
   if (seq < 0) return;
   const int mb = wave_uniform(rec_a.y), q_start = wave_uniform(rec_a.z), Lq = wave_uniform(rec_a.w);
