@@ -66,22 +66,54 @@ __device__ __forceinline__ int item_pieces(int n, int piece_tiles) {
 // Tiles [lo, hi) of piece j of k over n tiles (sizes differ by at most 1).
 __device__ __forceinline__ int piece_lo(int n, int k, int j) { return j * n / k; }
 
-// Inclusive scan over the 256 worker threads (4 waves); warp_tot holds 4 ints.
-__device__ __forceinline__ int block_incl_scan(int x, int* warp_tot, int& total) {
+// Inclusive prefix sum over the 64 lanes of a wave: inside each row of 16
+// lanes by DPP row shifts (a lane whose source is before its row's start
+// adds 0), then the totals of the rows before it (lanes 15, 31, 47) through
+// readlane.  No LDS round trip.
+__device__ __forceinline__ int wave_incl_scan(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+  const int row = (int)(threadIdx.x & 63) >> 4;
+  const int t0 = __builtin_amdgcn_readlane(x, 15), t1 = __builtin_amdgcn_readlane(x, 31);
+  const int t2 = __builtin_amdgcn_readlane(x, 47);
+  return x + (row >= 1 ? t0 : 0) + (row >= 2 ? t1 : 0) + (row >= 3 ? t2 : 0);
+}
+
+// Inclusive scans of two values over the 256 worker threads (4 waves; waves
+// past them get the workers' totals as their base), with one barrier: the
+// wave totals alternate between two halves of warp_tot (16 ints), so a
+// scan's totals are not overwritten before every wave has read them (the
+// scan two calls later writes them again only after the barrier of the scan
+// between, which every wave reaches after its reads).  `parity` is the
+// caller's alternation state, the same in every thread.
+__device__ __forceinline__ int2 block_incl_scan2(int2 x, int* warp_tot, int& parity, int2& total) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  int incl = x;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int o = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += o;
+  const int2 incl = make_int2(wave_incl_scan(x.x), wave_incl_scan(x.y));
+  int* buf = warp_tot + 8 * parity;
+  parity ^= 1;
+  if (tid < 256 && lane == 63) {
+    buf[wave] = incl.x;
+    buf[4 + wave] = incl.y;
   }
-  if (tid < 256 && lane == 63) warp_tot[wave] = incl;
   __syncthreads();
-  int base = 0;
-  for (int w = 0; w < wave && w < 4; ++w) base += warp_tot[w];
-  total = warp_tot[0] + warp_tot[1] + warp_tot[2] + warp_tot[3];
-  __syncthreads();
-  return base + incl;
+  int2 base = make_int2(0, 0);
+#pragma unroll
+  for (int w = 0; w < 4; ++w)
+    if (w < wave) {
+      base.x += buf[w];
+      base.y += buf[4 + w];
+    }
+  total = make_int2(buf[0] + buf[1] + buf[2] + buf[3], buf[4] + buf[5] + buf[6] + buf[7]);
+  return make_int2(base.x + incl.x, base.y + incl.y);
+}
+
+__device__ __forceinline__ int block_incl_scan(int x, int* warp_tot, int& parity, int& total) {
+  int2 t;
+  const int2 r = block_incl_scan2(make_int2(x, 0), warp_tot, parity, t);
+  total = t.x;
+  return r.x;
 }
 
 // Work list of the prefill kernel, written by one workgroup (256 threads or
@@ -103,11 +135,12 @@ __device__ __forceinline__ int block_incl_scan(int x, int* warp_tot, int& total)
 // at least kScheduleLdsInts ints (the workgroup that runs the schedule uses
 // no other LDS, so the caller lends it its own buffer).
 constexpr int kSchedCached = 4;
-constexpr int kScheduleLdsInts = kCostBuckets + 4;
+constexpr int kScheduleLdsInts = kCostBuckets + 16;
 
 __device__ __forceinline__ void prefill_schedule(const PrefillParams& p, PrefillItem* __restrict__ items, int* lds) {
   int* hist = lds;                    // [kCostBuckets]
-  int* warp_tot = lds + kCostBuckets;  // [4]
+  int* warp_tot = lds + kCostBuckets;  // [16]
+  int parity = 0;                      // block_incl_scan2's alternation
   const int tid = threadIdx.x;
   const bool worker = tid < 256;
   const int n_items_max = p.num_seqs * p.n_mblocks;
@@ -149,9 +182,9 @@ __device__ __forceinline__ void prefill_schedule(const PrefillParams& p, Prefill
     ++v;
     tt += n;
   });
-  int n_valid = 0, n_tiles_all = 0;
-  block_incl_scan(v, warp_tot, n_valid);
-  block_incl_scan(tt, warp_tot, n_tiles_all);
+  int2 vt;
+  block_incl_scan2(make_int2(v, tt), warp_tot, parity, vt);
+  const int n_valid = vt.x, n_tiles_all = vt.y;
   const bool split = n_valid > 0 && n_valid < p.slots_per_group;
   // piece length: from T / slots_per_group up, until the pieces fit one round
   int piece_tiles = split ? max(2, (n_tiles_all + p.slots_per_group - 1) / p.slots_per_group) : 0;
@@ -159,7 +192,7 @@ __device__ __forceinline__ void prefill_schedule(const PrefillParams& p, Prefill
     int np = 0;
     each_item([&](int n, const ItemGeom&, int) { np += item_pieces(n, piece_tiles); });
     int n_pieces = 0;
-    block_incl_scan(np, warp_tot, n_pieces);
+    block_incl_scan(np, warp_tot, parity, n_pieces);
     if (n_pieces <= p.slots_per_group) break;
     piece_tiles += max(1, piece_tiles / 4);
   }
@@ -181,7 +214,7 @@ __device__ __forceinline__ void prefill_schedule(const PrefillParams& p, Prefill
     }
   }
   int total = 0;
-  const int incl = block_incl_scan(sum, warp_tot, total);
+  const int incl = block_incl_scan(sum, warp_tot, parity, total);
   if (worker) {
     int run = incl - sum;
 #pragma unroll
@@ -198,11 +231,12 @@ __device__ __forceinline__ void prefill_schedule(const PrefillParams& p, Prefill
   auto scatter_round = [&](int n, const ItemGeom& g, int idx) {
     const int k = n >= 0 ? item_pieces(n, piece_tiles) : 0;
     const int ks = k > 1 ? k : 0;
-    int slots_total = 0, cnt_total = 0;
-    const int slot0 = slot_carry + block_incl_scan(ks, warp_tot, slots_total) - ks;
-    const int cnt0 = cnt_carry + block_incl_scan(ks > 0 ? 1 : 0, warp_tot, cnt_total) - (ks > 0 ? 1 : 0);
-    slot_carry += slots_total;
-    cnt_carry += cnt_total;
+    int2 tot;
+    const int2 inc = block_incl_scan2(make_int2(ks, ks > 0 ? 1 : 0), warp_tot, parity, tot);
+    const int slot0 = slot_carry + inc.x - ks;
+    const int cnt0 = cnt_carry + inc.y - (ks > 0 ? 1 : 0);
+    slot_carry += tot.x;
+    cnt_carry += tot.y;
     const int seq = idx / p.n_mblocks, mb = idx - seq * p.n_mblocks;
     for (int j = 0; j < k; ++j) {
       const int lo = piece_lo(n, k, j), hi = piece_lo(n, k, j + 1);
