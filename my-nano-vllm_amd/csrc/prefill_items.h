@@ -81,32 +81,44 @@ __device__ __forceinline__ int wave_incl_scan(int x) {
   return x + (row >= 1 ? t0 : 0) + (row >= 2 ? t1 : 0) + (row >= 3 ? t2 : 0);
 }
 
-// Inclusive scans of two values over the 256 worker threads (4 waves; waves
+// Inclusive scans of N values over the 256 worker threads (4 waves; waves
 // past them get the workers' totals as their base), with one barrier: the
-// wave totals alternate between two halves of warp_tot (16 ints), so a
-// scan's totals are not overwritten before every wave has read them (the
+// wave totals alternate between two halves of warp_tot (2 x 4 x N ints), so
+// a scan's totals are not overwritten before every wave has read them (the
 // scan two calls later writes them again only after the barrier of the scan
 // between, which every wave reaches after its reads).  `parity` is the
 // caller's alternation state, the same in every thread.
-__device__ __forceinline__ int2 block_incl_scan2(int2 x, int* warp_tot, int& parity, int2& total) {
+constexpr int kScanMaxValues = 4;
+template <int N>
+__device__ __forceinline__ void block_incl_scan_n(int (&x)[N], int* warp_tot, int& parity, int (&total)[N]) {
+  static_assert(N <= kScanMaxValues, "warp_tot holds kScanMaxValues values per wave");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int2 incl = make_int2(wave_incl_scan(x.x), wave_incl_scan(x.y));
-  int* buf = warp_tot + 8 * parity;
+  int incl[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) incl[i] = wave_incl_scan(x[i]);
+  int* buf = warp_tot + 4 * kScanMaxValues * parity;
   parity ^= 1;
   if (tid < 256 && lane == 63) {
-    buf[wave] = incl.x;
-    buf[4 + wave] = incl.y;
+#pragma unroll
+    for (int i = 0; i < N; ++i) buf[4 * i + wave] = incl[i];
   }
   __syncthreads();
-  int2 base = make_int2(0, 0);
 #pragma unroll
-  for (int w = 0; w < 4; ++w)
-    if (w < wave) {
-      base.x += buf[w];
-      base.y += buf[4 + w];
-    }
-  total = make_int2(buf[0] + buf[1] + buf[2] + buf[3], buf[4] + buf[5] + buf[6] + buf[7]);
-  return make_int2(base.x + incl.x, base.y + incl.y);
+  for (int i = 0; i < N; ++i) {
+    int base = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      if (w < wave) base += buf[4 * i + w];
+    total[i] = buf[4 * i] + buf[4 * i + 1] + buf[4 * i + 2] + buf[4 * i + 3];
+    x[i] = base + incl[i];
+  }
+}
+
+__device__ __forceinline__ int2 block_incl_scan2(int2 x, int* warp_tot, int& parity, int2& total) {
+  int v[2] = {x.x, x.y}, t[2];
+  block_incl_scan_n(v, warp_tot, parity, t);
+  total = make_int2(t[0], t[1]);
+  return make_int2(v[0], v[1]);
 }
 
 __device__ __forceinline__ int block_incl_scan(int x, int* warp_tot, int& parity, int& total) {
@@ -135,11 +147,11 @@ __device__ __forceinline__ int block_incl_scan(int x, int* warp_tot, int& parity
 // at least kScheduleLdsInts ints (the workgroup that runs the schedule uses
 // no other LDS, so the caller lends it its own buffer).
 constexpr int kSchedCached = 4;
-constexpr int kScheduleLdsInts = kCostBuckets + 16;
+constexpr int kScheduleLdsInts = kCostBuckets + 8 * kScanMaxValues;
 
 __device__ __forceinline__ void prefill_schedule(const PrefillParams& p, PrefillItem* __restrict__ items, int* lds) {
   int* hist = lds;                    // [kCostBuckets]
-  int* warp_tot = lds + kCostBuckets;  // [16]
+  int* warp_tot = lds + kCostBuckets;  // [8 * kScanMaxValues]
   int parity = 0;                      // block_incl_scan2's alternation
   const int tid = threadIdx.x;
   const bool worker = tid < 256;
@@ -186,15 +198,29 @@ __device__ __forceinline__ void prefill_schedule(const PrefillParams& p, Prefill
   block_incl_scan2(make_int2(v, tt), warp_tot, parity, vt);
   const int n_valid = vt.x, n_tiles_all = vt.y;
   const bool split = n_valid > 0 && n_valid < p.slots_per_group;
-  // piece length: from T / slots_per_group up, until the pieces fit one round
+  // piece length: from T / slots_per_group up (by a quarter, at least 1 tile,
+  // at most 16 times), until the pieces fit one round; four lengths are
+  // counted per scan
   int piece_tiles = split ? max(2, (n_tiles_all + p.slots_per_group - 1) / p.slots_per_group) : 0;
-  for (int iter = 0; split && iter < 16; ++iter) {
-    int np = 0;
-    each_item([&](int n, const ItemGeom&, int) { np += item_pieces(n, piece_tiles); });
-    int n_pieces = 0;
-    block_incl_scan(np, warp_tot, parity, n_pieces);
-    if (n_pieces <= p.slots_per_group) break;
-    piece_tiles += max(1, piece_tiles / 4);
+  for (int iter = 0; split && iter < 16; iter += 4) {
+    int cand[4], np[4] = {0, 0, 0, 0}, tot[4];
+    cand[0] = piece_tiles;
+#pragma unroll
+    for (int i = 1; i < 4; ++i) cand[i] = cand[i - 1] + max(1, cand[i - 1] / 4);
+    each_item([&](int n, const ItemGeom&, int) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) np[i] += item_pieces(n, cand[i]);
+    });
+    block_incl_scan_n(np, warp_tot, parity, tot);
+    int fit = 4;
+#pragma unroll
+    for (int i = 3; i >= 0; --i)
+      if (tot[i] <= p.slots_per_group) fit = i;
+    if (fit < 4) {
+      piece_tiles = cand[fit];
+      break;
+    }
+    piece_tiles = cand[3] + max(1, cand[3] / 4);
   }
   // histogram of piece sizes
   each_item([&](int n, const ItemGeom&, int) {
