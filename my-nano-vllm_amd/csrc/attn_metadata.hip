@@ -29,6 +29,7 @@
 // gets slot -1, and negative descriptor fields read as 0.
 #include <algorithm>
 
+#include "fp8_common.h"
 #include "kernels.h"
 
 namespace nvamd {
@@ -94,12 +95,7 @@ __global__ __launch_bounds__(kMetaThreads) void build_metadata_kernel(AttnMetaPa
   int incl[5];
 #pragma unroll
   for (int k = 0; k < 5; ++k) {
-    incl[k] = sum[k];
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int o = __shfl_up(incl[k], off, 64);
-      if (lane >= off) incl[k] += o;
-    }
+    incl[k] = wave_incl_scan(sum[k]);
     if (lane == 63) wave_tot[wave][k] = incl[k];
   }
   __syncthreads();

@@ -129,6 +129,21 @@ __device__ __forceinline__ float shfl_xor_f32(float v, int mask) {
   return __shfl_xor(v, mask, 64);
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave: inside each row of 16
+// lanes by DPP row shifts (a lane whose source is before its row's start
+// adds 0), then the totals of the rows before it (lanes 15, 31, 47) through
+// readlane.  No LDS round trip.
+__device__ __forceinline__ int wave_incl_scan(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+  const int row = (int)(threadIdx.x & 63) >> 4;
+  const int t0 = __builtin_amdgcn_readlane(x, 15), t1 = __builtin_amdgcn_readlane(x, 31);
+  const int t2 = __builtin_amdgcn_readlane(x, 47);
+  return x + (row >= 1 ? t0 : 0) + (row >= 2 ? t1 : 0) + (row >= 3 ? t2 : 0);
+}
+
 __device__ __forceinline__ int wave_uniform(int v) {
   return __builtin_amdgcn_readfirstlane(v);
 }

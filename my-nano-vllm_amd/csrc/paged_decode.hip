@@ -680,12 +680,7 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p, PrefillP
     const int L = (b < B) ? sk_seq_len<false>(p, b, cap) : 0;
     if (b < B) lens[b] = L;
     const int n = sk_stages(L);
-    int incl = n;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int o = __shfl_up(incl, off, 64);
-      if (lane >= off) incl += o;
-    }
+    const int incl = wave_incl_scan(n);  // DPP row shifts and readlane, no LDS round trip
     if (lane == 63) wtot[wave] = incl;
     __syncthreads();
     int wb = carry;
