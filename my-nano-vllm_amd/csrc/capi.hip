@@ -132,7 +132,11 @@ int short_cols(int G, int32_t max_seqlen_q) { return G * std::min(32 / G, std::m
 
 // kv heads per balanced-decode workgroup: whole 1 KiB cache rows when the
 // kv heads come in 8s (each workgroup then reads whole DRAM pages), else 4.
-int stream_k_heads(int32_t num_kv_heads) { return num_kv_heads % 8 == 0 ? 8 : 4; }
+// The short-query rows of a varlen call take 4: their pairs (sequence, kv
+// head group) are long against a workgroup's range, and with half as many
+// heads per pair each is cut among half as many workgroups, so its merge
+// reads half as many partials.
+int stream_k_heads(int32_t num_kv_heads, bool varlen) { return num_kv_heads % 8 == 0 && !varlen ? 8 : 4; }
 
 int stream_k_wgs(int ncb, int hg, int G, bool varlen) {
   return device_cu_count() * nvamd::decode_sk_wgs_per_cu(ncb, hg, G, varlen);
@@ -143,7 +147,7 @@ int stream_k_wgs(int ncb, int hg, int G, bool varlen) {
 // short-query rows of a varlen call).
 int64_t stream_k_prefix_bytes(int32_t batch) { return (((int64_t)batch + 1) * 4 + 255) / 256 * 256; }
 int64_t stream_k_bytes(int32_t batch, int32_t num_kv_heads, int32_t G, int cols, bool varlen) {
-  const int ncb = (cols + 15) / 16, hg = stream_k_heads(num_kv_heads);
+  const int ncb = (cols + 15) / 16, hg = stream_k_heads(num_kv_heads, varlen);
   return stream_k_prefix_bytes(batch) +
          (int64_t)stream_k_wgs(ncb, hg, G, varlen) * 2 * hg * cols * nvamd::kSkSlotFloats * (int64_t)sizeof(float);
 }
@@ -526,7 +530,7 @@ int32_t decode_attention(const char* fn, void* out, const void* q, const void* k
                   (long long)need, (long long)workspace_bytes);
     p.part_tokens = (int)std::min<int64_t>(kv_cap, 0x7fffffff);
     p.max_parts = 1;
-    p.sk_heads = stream_k_heads(num_kv_heads);
+    p.sk_heads = stream_k_heads(num_kv_heads, false);
     p.sk_wgs = stream_k_wgs(ncb, p.sk_heads, G, false);
     p.sk_cols = G;
     p.sk_prefix = static_cast<int32_t*>(workspace);
@@ -663,7 +667,7 @@ int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, con
   if (sk) {
     mp.part_tokens = (int)std::min<int64_t>(kv_cap, 0x7fffffff);
     mp.max_parts = 1;
-    mp.sk_heads = stream_k_heads(num_kv_heads);
+    mp.sk_heads = stream_k_heads(num_kv_heads, true);
     mp.sk_wgs = stream_k_wgs(ncb, mp.sk_heads, G, true);
     mp.sk_cols = short_cols(G, max_seqlen_q);
     mp.sk_prefix = static_cast<int32_t*>(workspace);

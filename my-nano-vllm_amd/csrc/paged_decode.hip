@@ -575,7 +575,7 @@ __global__ __launch_bounds__(256) void mq_reduce_varlen_kernel(MqParams p) {
 // short-query sequences of a paged varlen call (speculative-decode rows:
 // the Lq * G <= 32 query rows of a kv head are its MFMA columns, each with
 // its causal key limit; other sequences take no stages).  A pair =
-// (sequence b, group hg of HG kv heads, HG = 8 when Hkv % 8 == 0, else 4);
+// (sequence b, group hg of HG kv heads; HG = 8 for decode when Hkv % 8 == 0, else 4);
 // its n_b = ceil(L_b / 16) stages of 16 tokens are laid end to end in
 // (b, hg) order, T stages in all.  Workgroup w of a persistent grid of W
 // (as many as stay resident) streams a fixed share of about T/W stages
