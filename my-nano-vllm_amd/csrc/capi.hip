@@ -132,10 +132,10 @@ int short_cols(int G, int32_t max_seqlen_q) { return G * std::min(32 / G, std::m
 
 // kv heads per balanced-decode workgroup: whole 1 KiB cache rows when the
 // kv heads come in 8s (each workgroup then reads whole DRAM pages), else 4.
-// The short-query rows of a varlen call take 4: their pairs (sequence, kv
-// head group) are long against a workgroup's range, and with half as many
-// heads per pair each is cut among half as many workgroups, so its merge
-// reads half as many partials.
+// The short-query rows of a varlen call take 4: their workgroups read
+// their queries from global memory, which drains the ring at each pair
+// switch, and with 4 heads two half-size workgroups share a CU, so one keeps
+// streaming while the other drains.
 int stream_k_heads(int32_t num_kv_heads, bool varlen) { return num_kv_heads % 8 == 0 && !varlen ? 8 : 4; }
 
 int stream_k_wgs(int ncb, int hg, int G, bool varlen) {
