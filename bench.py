@@ -74,7 +74,7 @@ parity tests' checker) on the host cores for a bounded sample of the same
 workload; the prefill field carries one of its own.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--only decode|decode06|prefill|long|store|mixed|linear|metadata|lm_head|host|all]
+                    [--only FIELD[,FIELD...]]   (decode decode06 prefill long store mixed linear metadata lm_head host, or all)
                     [--no-cpu-baseline]
                     [--copy-probe]
 """
@@ -107,6 +107,7 @@ COPY_PROBE_BYTES = 1 << 30
 # the first tens of milliseconds, and the steady state is what a serving
 # loop sees.  The headline decode field keeps exactly --warmup warm-up calls.
 SECONDARY_WARM_S = 0.15
+FIELDS = ("decode", "decode06", "prefill", "long", "store", "mixed", "linear", "metadata", "lm_head", "host")
 
 
 def parse():
@@ -115,8 +116,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", default="all",
-                    choices=["decode", "decode06", "prefill", "long", "store", "mixed", "linear", "metadata", "lm_head",
-                             "host", "all"])
+                    help="comma-separated fields: " + ",".join(FIELDS) + " or all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 1 GiB device copy (counter scale for rocprofv3 --pmc)")
@@ -463,14 +463,14 @@ def bench_select_rows(steps, warmup):
     """LM-head row selection of the mixed step: 192 decode + 32 x 5 speculative
     rows + 3 prefill chunks of 512 (their last rows), hidden 4096, bf16."""
     from nanovllm_amd.layers.embed_head import select_lm_head_rows
-    from nanovllm_amd.utils.context import set_context, reset_context
+    from nanovllm_amd.utils.context import get_context, set_context, reset_context
     lq = [5] * 32 + [512] * 3
     cu = [0] + list(np.cumsum(lq))
     x = torch.randn(192 + cu[-1], 4096, device="cuda").to(torch.bfloat16)
     set_context(split_pt=192, num_spec_seqs=32, num_spec_rows=160,
                 cu_seqlens_q=torch.tensor(cu, dtype=torch.int32, device="cuda"))
     try:
-        ms = timed(lambda i: select_lm_head_rows(x), steps, warmup)
+        ms = timed(lambda i: select_lm_head_rows(x, get_context()), steps, warmup)
     finally:
         reset_context()
     return dict(ms=ms, rows=192 + 160 + 3)
@@ -528,11 +528,12 @@ def bench_metadata(wl, steps=200, warmup=20):
     vectorised host build, and the GPU time of the on-device build's upload +
     kernel (HIP events on the current stream)."""
     from nanovllm_amd.engine import metadata as nm
+    from nanovllm_amd.utils.context import set_context
     dseqs, pseqs = step_sequences(wl)
     bs = wl.block_size
     res = {}
-    for name, fn in (("device", lambda: nm.prepare_sequence_device(dseqs, pseqs, bs)),
-                     ("host_numpy", lambda: nm.prepare_sequence(dseqs, pseqs, bs))):
+    for name, fn in (("device", lambda: nm.prepare_sequence_device(dseqs, pseqs, bs, set_context)),
+                     ("host_numpy", lambda: nm.prepare_sequence(dseqs, pseqs, bs, set_context))):
         for _ in range(warmup):
             fn()
         torch.cuda.synchronize()
@@ -674,6 +675,15 @@ def _traffic_from_profile():
 
 def main():
     args = parse()
+    only = set(args.only.split(","))
+    unknown = only - set(FIELDS) - {"all"}
+    if unknown:
+        print(f"bench.py: unknown --only field(s) {sorted(unknown)}; choose from {FIELDS} or all", file=sys.stderr)
+        sys.exit(2)
+
+    def want(field):
+        return "all" in only or field in only
+
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build has no "
               "multi-GPU path; run with --gpus 1", file=sys.stderr)
@@ -687,7 +697,7 @@ def main():
     if args.copy_probe:
         copy_probe()
 
-    if args.only in ("decode", "all"):
+    if want("decode"):
         wl = W.qwen3_8b_decode()
         log(f"decode workload {wl.name}: B={wl.num_seqs} bytes={wl.decode_bytes()}")
         res, pools, q = bench_decode(wl, args.steps, args.warmup)
@@ -709,7 +719,7 @@ def main():
         del pools
         torch.cuda.empty_cache()
 
-    if args.only in ("decode06", "all"):
+    if want("decode06"):
         wl = W.qwen3_0p6b_decode()
         log(f"decode workload {wl.name}: B={wl.num_seqs} bytes={wl.decode_bytes()}")
         res, pools, q = bench_decode(wl, args.steps, args.warmup)
@@ -722,7 +732,7 @@ def main():
         del pools
         torch.cuda.empty_cache()
 
-    if args.only in ("prefill", "all"):
+    if want("prefill"):
         wl = W.qwen3_8b_prefill()
         log(f"prefill workload {wl.name}: flops={wl.attention_flops()}")
         res, pools, q = bench_prefill(wl, max(args.steps // 2, 5), max(args.warmup // 2, 2), warm_s=SECONDARY_WARM_S)
@@ -746,7 +756,7 @@ def main():
         del pools, q
         torch.cuda.empty_cache()
 
-    if args.only in ("store", "all"):
+    if want("store"):
         wl = W.qwen3_8b_prefill()
         res = bench_store(wl, max(args.steps, 20), max(args.warmup, 5))
         log(f"store: {res['ms'] * 1e3:.1f} us/step, {res['gbs']:.1f} GB/s")
@@ -756,7 +766,7 @@ def main():
                               kernels="kv_store_fp8_kernel")
         torch.cuda.empty_cache()
 
-    if args.only in ("store", "all"):
+    if want("store"):
         wl = W.qwen3_8b_prefill()
         res = bench_qk_norm_rope(wl, max(args.steps, 20), max(args.warmup, 5))
         log(f"fused q/k norm + rope + store: {res['ms'] * 1e3:.1f} us/step, {res['gbs']:.1f} GB/s")
@@ -766,7 +776,7 @@ def main():
             algorithmic_bytes_per_step=res["bytes"], kernels="qk_norm_rope_store_kernel")
         torch.cuda.empty_cache()
 
-    if args.only in ("mixed", "all"):
+    if want("mixed"):
         full = W.qwen3_8b_mixed()
         varlen = W.sub_workload(full, range(full.extra["split_pt"], full.num_seqs), name="qwen3_8b_mixed_varlen")
         spec = W.sub_workload(full, range(full.extra["split_pt"], full.extra["split_pt"] + full.extra["num_spec_seqs"]),
@@ -797,7 +807,7 @@ def main():
             kernels="varlen_prefill_kernel<false>")
         torch.cuda.empty_cache()
 
-    if args.only in ("long", "all"):
+    if want("long"):
         wl = W.qwen3_32b_long_decode()
         log(f"long decode workload {wl.name}: bytes={wl.decode_bytes()}")
         res, pools, _ = bench_decode(wl, max(args.steps // 5, 5), max(args.warmup // 5, 2), n_pools=1,
@@ -810,7 +820,7 @@ def main():
         del pools
         torch.cuda.empty_cache()
 
-    if args.only in ("linear", "all"):
+    if want("linear"):
         # Qwen3-8B FP8 checkpoints: the qkv projection of a 16 x 512-token
         # prefill step (MFMA-bound) and the gate/up projection of the mixed
         # batch's 192 decode rows (weight-streaming, HBM-bound)
@@ -836,7 +846,7 @@ def main():
             extra["fp8_linear"]["cpu_baseline"] = cpu_baseline_fp8_linear(6144, 4096)
         torch.cuda.empty_cache()
 
-    if args.only in ("metadata", "all"):
+    if want("metadata"):
         out = {}
         for wl in (W.qwen3_8b_mixed(), W.qwen3_8b_prefill()):
             res, dseqs, pseqs = bench_metadata(wl)
@@ -849,7 +859,7 @@ def main():
         extra["metadata"] = dict(workload="one engine step's attention metadata (mixed batch; 16 x 512 prefill)",
                                  kernels="build_metadata_kernel", **out)
 
-    if args.only in ("lm_head", "all"):
+    if want("lm_head"):
         res = bench_sampler(355, 151936, max(args.steps, 20), max(args.warmup, 5))
         sel = bench_select_rows(max(args.steps, 20), max(args.warmup, 5))
         log(f"sampler: {res['ms'] * 1e3:.1f} us ({res['gbs']:.0f} GB/s), reference arithmetic in torch "
@@ -866,7 +876,7 @@ def main():
             extra["lm_head"]["cpu_baseline"] = cpu_baseline_sampler(151936)
         torch.cuda.empty_cache()
 
-    if args.only in ("host", "all"):
+    if want("host"):
         res = bench_host_overhead()
         log("host time per call: " + ", ".join(f"{k} {v} us" for k, v in res.items() if isinstance(v, float)))
         extra["host_overhead"] = dict(

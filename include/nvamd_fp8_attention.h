@@ -94,7 +94,9 @@ int32_t nvamd_store_kvcache(const void* key, int64_t key_stride0,
  * q_out: bf16 [num_tokens, num_heads, head_dim] = RoPE(RMSNorm(q)).
  * k_out: bf16 [num_tokens, num_kv_heads, head_dim] = RoPE(RMSNorm(k)), or NULL.
  * k_cache / v_cache, slot_mapping, num_slots: as nvamd_store_kvcache; the
- *   cache receives E4M3FN(RoPE(RMSNorm(k))) and E4M3FN(v).
+ *   cache receives E4M3FN(RoPE(RMSNorm(k))) and E4M3FN(v).  num_slots == 0
+ *   (no cache allocated yet: the runner's warm-up, model_runner.py:35-36)
+ *   stores nothing, and the three pointers may then be NULL.
  * head_dim must be 128; num_heads + 2 * num_kv_heads at most 128; tensors
  * 16-byte aligned (caches 8).
  */

@@ -141,8 +141,11 @@ __global__ __launch_bounds__(kMetaThreads) void build_metadata_kernel(AttnMetaPa
         const int64_t len = ds.x;
         const int64_t nb = (len + bs - 1) / bs;
         p.positions[u] = len - 1;
-        if (ds.w > 0 && slot_off[s] < p.cap_slots)
-          p.slot_mapping[slot_off[s]] = (int32_t)(entry(toff[s], ds.w - 1) * bs + (len - (nb - 1) * bs) - 1);
+        // a plain decode row always owns one slot entry; without a block table
+        // (which the reference's loops cannot handle) it is -1, so the store skips it
+        if (slot_off[s] < p.cap_slots)
+          p.slot_mapping[slot_off[s]] =
+              ds.w > 0 ? (int32_t)(entry(toff[s], ds.w - 1) * bs + (len - (nb - 1) * bs) - 1) : -1;
       } else {
         const int64_t i = u - pos_off[s], pos = (int64_t)ds.y + i;
         p.positions[u] = pos;

@@ -251,8 +251,8 @@ int32_t nvamd_qk_norm_rope_store(const void* qkv, int64_t qkv_stride0, const int
   if (qkv_stride0 < (int64_t)(num_heads + 2 * num_kv_heads) * head_dim)
     return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: qkv row stride %lld is shorter than a row", fn, (long long)qkv_stride0);
   if (num_tokens == 0) return ok();
-  if (!qkv || !positions || !q_norm_weight || !k_norm_weight || !cos_sin_cache || !q_out || !k_cache || !v_cache ||
-      !slot_mapping)
+  if (!qkv || !positions || !q_norm_weight || !k_norm_weight || !cos_sin_cache || !q_out ||
+      (num_slots > 0 && (!k_cache || !v_cache || !slot_mapping)))
     return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
   if (qkv_stride0 % 8 != 0 || (uintptr_t)qkv % 16 != 0 || (uintptr_t)q_out % 16 != 0 ||
       (k_out && (uintptr_t)k_out % 16 != 0) || (uintptr_t)q_norm_weight % 16 != 0 ||

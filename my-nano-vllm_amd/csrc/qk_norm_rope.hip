@@ -77,7 +77,9 @@ __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(QkNormRopeParam
   const int64_t tok = blockIdx.x;
   const int g = (int)(threadIdx.x >> 4);
   const int j = (int)(threadIdx.x & 15);
-  const int32_t slot = p.slot_mapping[tok];
+  // num_slots == 0: no cache yet (the runner's warm-up), nothing is stored and
+  // slot_mapping may be null
+  const int32_t slot = p.num_slots > 0 ? p.slot_mapping[tok] : -1;
   const bool store = slot >= 0 && (int64_t)slot < p.num_slots;
   const int64_t cache_row = (int64_t)slot * p.Hkv * kHeadDim;
   int64_t pos = p.positions[tok];

@@ -28,6 +28,13 @@ the number of sequences and blocks, none per token), uploads it with one
 pinned non-blocking copy, and ``nvamd_build_attention_metadata`` expands it
 into positions, slot mapping, context lengths, cu_seqlens and the padded
 block tables.
+
+Both builders publish the step through the ``set_context`` they are given:
+the caller names the Context its attention and LM-head layers read.  Inside
+nano-vLLM's runner that is ``nanovllm.utils.context.set_context``; the
+package's own ``nanovllm_amd.utils.context.set_context`` also receives the
+host-side ``num_spec_rows``.  There is no default, so a step is never
+published to a Context nobody reads.
 """
 import itertools
 from dataclasses import dataclass
@@ -35,7 +42,21 @@ from dataclasses import dataclass
 import numpy as np
 import torch
 
-from ..utils.context import set_context
+from ..utils import context as _pkg_context
+
+# the fields of nanovllm/utils/context.py:5-15 (what any Context accepts)
+_REFERENCE_FIELDS = ("split_pt", "num_spec_seqs", "cu_seqlens_q", "cu_seqlens_k", "max_seqlen_q", "max_seqlen_k",
+                     "slot_mapping", "context_lens", "block_tables")
+
+
+def _publish(set_context, fields, num_spec_rows):
+    if not callable(set_context):
+        raise TypeError("set_context must be the Context setter the step's layers read "
+                        "(nanovllm.utils.context.set_context inside nano-vLLM's runner)")
+    values = {k: fields[k] for k in _REFERENCE_FIELDS}
+    if set_context is _pkg_context.set_context:
+        values["num_spec_rows"] = num_spec_rows
+    set_context(**values)
 
 
 def _seq_len(seq):
@@ -133,20 +154,20 @@ def _to_device(arr, device):
     return t.to(device)
 
 
-def prepare_sequence(dseqs, pseqs, block_size, device="cuda"):
-    """Builds the step's metadata, publishes it through the Context and returns
-    the device positions (model_runner.prepare_sequence, :203-220)."""
+def prepare_sequence(dseqs, pseqs, block_size, set_context, device="cuda"):
+    """Builds the step's metadata, publishes it through ``set_context`` and
+    returns the device positions (model_runner.prepare_sequence, :203-220)."""
     md = build_host_metadata(dseqs, pseqs, block_size)
     has_varlen = md.cu_seqlens_q.size > 0
     num_spec_rows = sum(s.num_scheduled_tokens for s in dseqs if s.num_scheduled_tokens > 1)
-    set_context(
-        split_pt=md.split_pt, num_spec_seqs=md.num_spec_seqs, num_spec_rows=num_spec_rows,
+    _publish(set_context, dict(
+        split_pt=md.split_pt, num_spec_seqs=md.num_spec_seqs,
         slot_mapping=_to_device(md.slot_mapping, device),
         context_lens=_to_device(md.context_lens, device) if md.split_pt else None,
         cu_seqlens_q=_to_device(md.cu_seqlens_q, device) if has_varlen else None,
         cu_seqlens_k=_to_device(md.cu_seqlens_k, device) if has_varlen else None,
         max_seqlen_q=md.max_seqlen_q, max_seqlen_k=md.max_seqlen_k,
-        block_tables=_to_device(md.block_tables, device))
+        block_tables=_to_device(md.block_tables, device)), num_spec_rows)
     return _to_device(md.positions, device)
 
 
@@ -234,10 +255,9 @@ def build_device_metadata(step: PackedStep, block_size, device="cuda"):
                 num_spec_seqs=step.num_spec, num_spec_rows=step.num_spec_rows)
 
 
-def prepare_sequence_device(dseqs, pseqs, block_size, device="cuda"):
+def prepare_sequence_device(dseqs, pseqs, block_size, set_context, device="cuda"):
     """prepare_sequence with the metadata built on the GPU: publishes it
-    through the Context and returns the device positions."""
+    through ``set_context`` and returns the device positions."""
     md = build_device_metadata(pack_step(dseqs, pseqs, block_size), block_size, device)
-    positions = md.pop("positions")
-    set_context(**md)
-    return positions
+    _publish(set_context, md, md["num_spec_rows"])
+    return md["positions"]

@@ -6,20 +6,24 @@ row of the speculative sequences (their drafts are verified against all of
 them) and the last row of each prefill sequence.  ``select_lm_head_rows``
 builds that matrix with one HIP gather (``nvamd_select_logit_rows``) from
 the step's Context; ``lm_head_logits`` then applies the bf16 LM-head weight
-(a plain library GEMM, as F.linear in the reference).  The speculative row
-count comes from the Context's host-side ``num_spec_rows`` when the
-metadata builder set it (the reference reads ``cu_seqlens_q[nspec]`` back
-from the GPU).
+(a plain library GEMM, as F.linear in the reference).
+
+The Context is an argument: the caller passes the one its runner filled
+(inside nano-vLLM, ``nanovllm.utils.context.get_context()``, the object
+ParallelLMHead.forward reads at :57).  The speculative row count comes from
+the Context's host-side ``num_spec_rows`` when it has one and the metadata
+builder set it; otherwise ``cu_seqlens_q[nspec]`` is read back from the GPU,
+as the reference does (:63).
 """
 import torch
 import torch.nn.functional as F
 
 from .. import _native
-from ..utils.context import get_context
 
 
-def select_lm_head_rows(x: torch.Tensor) -> torch.Tensor:
-    context = get_context()
+def select_lm_head_rows(x: torch.Tensor, context) -> torch.Tensor:
+    """The rows of ``x`` the LM head keeps under ``context`` (a Context with
+    the fields of nanovllm/utils/context.py:5-15)."""
     cu = context.cu_seqlens_q
     if not isinstance(cu, torch.Tensor):
         return x
@@ -29,7 +33,9 @@ def select_lm_head_rows(x: torch.Tensor) -> torch.Tensor:
         raise ValueError(f"x must be bf16, fp16 or fp32 (got {x.dtype})")
     split_pt, nspec = context.split_pt, context.num_spec_seqs
     n_var = cu.numel() - 1
-    n_spec_rows = context.num_spec_rows if context.num_spec_rows >= 0 else int(cu[nspec].item())
+    n_spec_rows = getattr(context, "num_spec_rows", -1)
+    if n_spec_rows < 0:
+        n_spec_rows = int(cu[nspec].item())
     n_prefill = n_var - nspec
     if x.stride(-1) != 1 or (x.stride(0) * x.element_size()) % 16 or x.data_ptr() % 16:
         x = x.contiguous()
@@ -43,6 +49,6 @@ def select_lm_head_rows(x: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def lm_head_logits(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+def lm_head_logits(x: torch.Tensor, weight: torch.Tensor, context) -> torch.Tensor:
     """The logits ParallelLMHead.forward returns on one GPU (embed_head.py:56-73)."""
-    return F.linear(select_lm_head_rows(x), weight)
+    return F.linear(select_lm_head_rows(x, context), weight)

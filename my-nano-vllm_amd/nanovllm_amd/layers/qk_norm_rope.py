@@ -10,10 +10,15 @@ the steps between the QKV projection and the attention call::
 
 with one gfx950 kernel that reads each head row of ``qkv`` once, returns
 the normalised, rotated q (bf16) and writes k and v straight into the FP8
-cache.  The attention call that follows then skips its own store (see
-INTEGRATION.md).  The arithmetic keeps the reference's rounding points
-(fp32 math, bf16 after the normalisation, after the weight product and
-after the rotation).
+cache.  The attention call that follows then skips its own store.  The
+arithmetic keeps the reference's rounding points (fp32 math, bf16 after the
+normalisation, after the weight product and after the rotation).
+
+Before the runner allocates the cache (its warm-up runs first,
+model_runner.py:35-36) the layer's caches are empty ``torch.tensor([])``:
+then nothing is stored, ``slot_mapping`` is ignored, and the caller asks for
+k as well (``return_k=True``), which the contiguous prefill path needs
+beside v.
 """
 import torch
 
@@ -39,8 +44,10 @@ def qk_norm_rope_store(positions: torch.Tensor, qkv: torch.Tensor, q_norm_weight
         eps: RMSNorm epsilon
         cos_sin_cache: [max_position, head_dim] or [max_position, 1, head_dim] fp32
             (RotaryEmbedding.cos_sin_cache)
-        k_cache, v_cache: [num_blocks, block_size, num_kv_heads, head_dim] FP8 E4M3FN
-        slot_mapping: [N] int32; -1 stores nothing for that token
+        k_cache, v_cache: [num_blocks, block_size, num_kv_heads, head_dim] FP8 E4M3FN,
+            or both empty (numel() == 0) or None: no store
+        slot_mapping: [N] int32; -1 stores nothing for that token (ignored
+            without a cache)
     Returns:
         q: [N, num_heads, head_dim] bf16 = RoPE(RMSNorm(q)); with return_k
         also k: [N, num_kv_heads, head_dim] bf16 = RoPE(RMSNorm(k)).
@@ -59,23 +66,35 @@ def qk_norm_rope_store(positions: torch.Tensor, qkv: torch.Tensor, q_norm_weight
     cs = cos_sin_cache.reshape(cos_sin_cache.shape[0], -1).contiguous()
     if cs.shape[1] != head_dim:
         raise ValueError("cos_sin_cache rows must hold head_dim values (cos then sin)")
-    _check(k_cache, "k_cache", torch.float8_e4m3fn, dev)
-    _check(v_cache, "v_cache", torch.float8_e4m3fn, dev)
-    if v_cache.shape != k_cache.shape or not (k_cache.is_contiguous() and v_cache.is_contiguous()):
-        raise ValueError("k_cache/v_cache must be contiguous and of one shape")
-    if k_cache.shape[-2] * k_cache.shape[-1] != num_kv_heads * head_dim:
-        raise ValueError("cache rows do not hold num_kv_heads * head_dim values")
+    no_cache = [c is None or c.numel() == 0 for c in (k_cache, v_cache)]
+    if no_cache[0] != no_cache[1]:
+        raise ValueError("k_cache and v_cache must both be allocated or both be empty")
+    has_cache = not no_cache[0]
+    if has_cache:
+        _check(k_cache, "k_cache", torch.float8_e4m3fn, dev)
+        _check(v_cache, "v_cache", torch.float8_e4m3fn, dev)
+        if v_cache.shape != k_cache.shape or not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+            raise ValueError("k_cache/v_cache must be contiguous and of one shape")
+        if k_cache.shape[-2] * k_cache.shape[-1] != num_kv_heads * head_dim:
+            raise ValueError("cache rows do not hold num_kv_heads * head_dim values")
     pos = positions.to(device=dev, dtype=torch.int64).contiguous()
-    slots = slot_mapping.to(device=dev, dtype=torch.int32).contiguous()
-    if pos.numel() != n or slots.numel() != n:
-        raise ValueError("positions and slot_mapping need one entry per token")
+    if pos.numel() != n:
+        raise ValueError("positions need one entry per token")
+    if has_cache:
+        slots = slot_mapping.to(device=dev, dtype=torch.int32).contiguous()
+        if slots.numel() != n:
+            raise ValueError("slot_mapping needs one entry per token")
     wq, wk = q_norm_weight.contiguous(), k_norm_weight.contiguous()  # held until the launch is enqueued
     q = torch.empty(n, num_heads, head_dim, dtype=torch.bfloat16, device=dev)
     k = torch.empty(n, num_kv_heads, head_dim, dtype=torch.bfloat16, device=dev) if return_k else None
-    num_slots = k_cache.numel() // (num_kv_heads * head_dim)
+    if has_cache:
+        num_slots = k_cache.numel() // (num_kv_heads * head_dim)
+        kc, vc, sl = k_cache.data_ptr(), v_cache.data_ptr(), slots.data_ptr()
+    else:
+        num_slots, kc, vc, sl = 0, None, None, None
     status = lib.nvamd_qk_norm_rope_store(
-        qkv.data_ptr(), qkv.stride(0), pos.data_ptr(), wq.data_ptr(), wk.data_ptr(), float(eps), cs.data_ptr(), cs.shape[0], q.data_ptr(),
-        k.data_ptr() if k is not None else None, k_cache.data_ptr(), v_cache.data_ptr(), slots.data_ptr(), n,
+        qkv.data_ptr(), qkv.stride(0), pos.data_ptr(), wq.data_ptr(), wk.data_ptr(), float(eps), cs.data_ptr(),
+        cs.shape[0], q.data_ptr(), k.data_ptr() if k is not None else None, kc, vc, sl, n,
         num_heads, num_kv_heads, head_dim, num_slots, torch.cuda.current_stream(dev).cuda_stream)
     _native.check(status, "qk_norm_rope_store")
     return (q, k) if return_k else q

@@ -24,7 +24,7 @@ from torch import nn
 
 from nanovllm_amd.engine.metadata import prepare_sequence
 from attention_layer import Attention
-from nanovllm_amd.utils.context import get_context, reset_context
+from nanovllm_amd.utils.context import get_context, reset_context, set_context
 from oracle import attention as oa
 from oracle import fp8 as ofp8
 
@@ -208,7 +208,7 @@ class GreedyRunner:
         for _, s in spec:
             s.num_cached_tokens = len(s.tokens) - 1
             s.tokens = s.tokens + s.drafts
-        positions = prepare_sequence([s for _, s in plain + spec], [s for _, s in pseqs], self.bs)
+        positions = prepare_sequence([s for _, s in plain + spec], [s for _, s in pseqs], self.bs, set_context)
         input_ids = torch.tensor(ids, dtype=torch.int64, device="cuda")
         hidden = self.model.forward(input_ids, positions)
         logits = self.model.logits(hidden)
@@ -238,3 +238,49 @@ def make_sequences(prompt_lens, max_new, vocab, block_size, num_blocks, seed):
         table, pool = pool[:nb], pool[nb:]
         seqs.append(Seq(tokens=rng.integers(0, vocab, size=L).tolist(), block_table=table, prompt_len=L))
     return seqs
+
+
+class GreedyComparison:
+    """Row-by-row comparison of two greedy runs (product vs oracle) with a
+    margin bound fixed in advance.  ``check(step, i, lh, lo)`` takes one
+    sequence's predicting rows of one step ([n, vocab] logits of the product
+    run and of the oracle run) and returns the token both runs feed back.
+
+    * Every row must give the same greedy token in both runs unless the
+      oracle's top-2 margin there is below ``margin_bound`` (a numerical tie);
+      a flip at a larger margin raises AssertionError.
+    * Each run feeds back its own greedy token (free-running).  Where the
+      fed-back row (row 0) flips at a tie, both runs continue with the
+      oracle's token from there (teacher-forced at that row), so their inputs
+      stay identical and every later row is still compared.
+    * Every row's logits must agree within ``logit_tol``.
+    """
+
+    def __init__(self, margin_bound, logit_tol):
+        self.margin_bound, self.logit_tol = margin_bound, logit_tol
+        self.flips, self.forced = [], []
+        self.worst, self.n_rows, self.ties = 0.0, 0, 0
+
+    def check(self, step, i, lh, lo):
+        lh, lo = lh.float().cpu(), lo.float().cpu()
+        assert lh.shape == lo.shape
+        th, to = lh.argmax(-1).tolist(), lo.argmax(-1).tolist()
+        dev = (lh - lo).abs().max(dim=-1).values
+        self.worst = max(self.worst, float(dev.max()))
+        assert torch.allclose(lh, lo, **self.logit_tol), \
+            f"step {step} seq {i}: logits differ by up to {float(dev.max())}"
+        top2 = lo.topk(2, dim=-1).values
+        margins = (top2[:, 0] - top2[:, 1]).tolist()
+        for r, (a, b, mg, dv) in enumerate(zip(th, to, margins, dev.tolist())):
+            self.n_rows += 1
+            self.ties += mg < self.margin_bound
+            if a != b:
+                assert mg < self.margin_bound, (
+                    f"step {step} seq {i} row {r}: product greedy token {a} != oracle {b} at oracle top-2 margin "
+                    f"{mg:.4f} >= {self.margin_bound} (row |dlogit| {dv:.4f})")
+                self.flips.append((step, i, r, round(mg, 4), round(dv, 4)))
+                print(f"[qwen3-greedy] tie flip: step {step} seq {i} row {r}: margin {mg:.4f}, "
+                      f"|dlogit| {dv:.4f}", flush=True)
+        if th[0] != to[0]:
+            self.forced.append((step, i))
+        return to[0]

@@ -59,17 +59,8 @@ def _step_inputs(wl, B):
     return ids, pos, slot, ctx, bt
 
 
-@pytest.mark.parametrize("B", [3, 16, 40])
-def test_graph_replay_matches_eager(B):
-    announce(f"graph: capture + replay B={B}")
-    L, Hq, Hkv = 2, 16, 8
-    model = TinyAttnStack(L, Hq, Hkv).cuda()
-    wl = W.qwen3_0p6b_decode(B=64)
-    max_nb = 8  # 2048 tokens
-    runner = DecodeGraphRunner(model, max_bs=48, max_num_blocks=max_nb, hidden_size=Hq * 128)
-    kv = _setup(model, L, wl.num_blocks)
-    runner.capture()
-    for rep in range(3):
+def _replay_vs_eager(model, runner, kv, wl, B, reps=3):
+    for rep in range(reps):
         ids, pos, slot, ctx, bt = _step_inputs(wl, B)
         ctx = torch.clamp(ctx - rep * 7, min=1)          # mutate contexts between replays
         slot = slot - 0                                   # same slots
@@ -84,3 +75,37 @@ def test_graph_replay_matches_eager(B):
         reset_context()
         assert torch.equal(kv.view(torch.uint8), kv_eager.view(torch.uint8)), f"cache differs (replay {rep})"
         assert torch.equal(replayed, eager), f"replay {rep} differs from eager"
+
+
+@pytest.mark.parametrize("B", [3, 16, 40])
+def test_graph_replay_matches_eager(B):
+    announce(f"graph: capture + replay B={B}")
+    L, Hq, Hkv = 2, 16, 8
+    model = TinyAttnStack(L, Hq, Hkv).cuda()
+    wl = W.qwen3_0p6b_decode(B=64)
+    max_nb = 8  # 2048 tokens
+    runner = DecodeGraphRunner(model, max_bs=48, max_num_blocks=max_nb, hidden_size=Hq * 128)
+    kv = _setup(model, L, wl.num_blocks)
+    runner.capture()
+    _replay_vs_eager(model, runner, kv, wl, B)
+
+
+def test_graph_replay_qwen3_8b_headline_shapes():
+    """The reference's capture list up to max_bs = 256 (1, 2, 4, 8, 16, ..., 256,
+    model_runner.py:306) at Qwen3-8B heads (32/8) with 16-block tables (4,096
+    tokens at block size 256); a 192-row step (the headline decode batch,
+    context U[256, 4096]) replays the 192 graph and must equal eager, on three
+    replays with mutated context lengths; then a 100-row step pads into the
+    112 graph."""
+    announce("graph: capture 1..256 at 32/8 heads, max_num_blocks 16; replay B=192 and B=100")
+    L, Hq, Hkv = 2, 32, 8
+    model = TinyAttnStack(L, Hq, Hkv).cuda()
+    wl = W.qwen3_8b_decode()
+    assert wl.num_seqs == 192 and wl.block_tables.shape[1] <= 16
+    runner = DecodeGraphRunner(model, max_bs=256, max_num_blocks=16, hidden_size=Hq * 128)
+    assert runner.graph_bs == [1, 2, 4, 8] + list(range(16, 257, 16))
+    kv = _setup(model, L, wl.num_blocks)
+    runner.capture()
+    assert runner.pick(192) == 192 and runner.pick(100) == 112
+    _replay_vs_eager(model, runner, kv, wl, 192)
+    _replay_vs_eager(model, runner, kv, wl, 100, reps=1)

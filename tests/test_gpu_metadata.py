@@ -92,10 +92,31 @@ def test_prepare_sequence_device_sets_the_context():
     rng = np.random.default_rng(3)
     dseqs, pseqs = random_step(rng, 256, 10, 3)
     want = om.prepare_sequence(dseqs, pseqs, 256)
-    positions = nm.prepare_sequence_device(dseqs, pseqs, 256)
+    positions = nm.prepare_sequence_device(dseqs, pseqs, 256, ctxmod.set_context)
     c = ctxmod.get_context()
     torch.cuda.synchronize()
     assert positions.cpu().tolist() == want["positions"]
     assert c.slot_mapping.cpu().tolist() == want["slot_mapping"] and c.split_pt == want["split_pt"]
     assert c.block_tables.cpu().tolist() == want["block_tables"]
     ctxmod.reset_context()
+
+
+def test_plain_row_without_a_table_gets_slot_minus_one():
+    """The C ABI accepts a plain decode descriptor with table_len 0 (pack_step
+    rejects it, as the reference's block_table[-1] would fail): its slot
+    entry is written as -1, so a store skips it, instead of left unset."""
+    announce("metadata: plain decode descriptor without a table")
+    seqs = [om.SeqView(300, 299, 1, [7, 9]), om.SeqView(40, 39, 1, [11])]
+    step = nm.pack_step(seqs, [], 256)
+    desc = step.packed[:8].reshape(2, 4).copy()
+    desc[1, 3] = 0                                    # second row: no table
+    packed = np.concatenate([desc.reshape(-1), step.packed[8:10]]).astype(np.int32)
+    bad = nm.PackedStep(packed=packed, num_seqs=2, num_plain=2, num_spec=0, num_tokens=2, num_slots=2,
+                        num_table_rows=1, max_table_len=2, max_seqlen_q=0, max_seqlen_k=0, num_spec_rows=0)
+    for _ in range(3):   # the slot buffer comes from the caching allocator, so it holds old values
+        got = nm.build_device_metadata(bad, 256)
+        torch.cuda.synchronize()
+        assert got["slot_mapping"].cpu().tolist() == [9 * 256 + 43, -1]
+        assert got["positions"].cpu().tolist() == [299, 39]
+        assert got["context_lens"].cpu().tolist() == [300, 40]
+        assert got["block_tables"].cpu().tolist() == [[7, 9]]

@@ -94,3 +94,32 @@ def test_ragged_shapes_padding_slots_and_strided_rows(n, hq, hkv):
     announce(f"qk_norm_rope_store: N={n}, {hq}/{hkv} heads")
     res = _case(n, hq, hkv, slots, positions, max_pos, nb, bs=bs, seed=n, row_pad=64, scale=4.0)
     _check(res, hq, hkv, slots, f"N={n} {hq}/{hkv}")
+
+
+def test_warmup_without_a_cache():
+    """The runner's warm-up runs the model before the cache exists
+    (model_runner.py:35-36): the layer's caches are torch.tensor([]) (fp32,
+    one dimension, empty) and warm-up sequences have no slots.  Nothing is
+    stored, and q and k are returned for the contiguous prefill path."""
+    announce("qk_norm_rope_store: warm-up, empty caches and no slots")
+    n, hq, hkv, max_pos = 300, 32, 8, 4096
+    g = torch.Generator().manual_seed(17)
+    qkv_cpu = torch.randn(n, (hq + 2 * hkv) * D, generator=g).to(torch.bfloat16)
+    wq = (1.0 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    wk = (1.0 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    cache = oq.rope_cache(D, max_pos, 1e6)
+    positions = torch.arange(n, dtype=torch.int64)
+    kc_cpu = torch.zeros(1, 16, hkv, D, dtype=torch.uint8)
+    q_want, k_want = oq.qk_norm_rope_store(qkv_cpu, hq, hkv, D, positions, wq, wk, 1e-6, cache, kc_cpu,
+                                           torch.zeros_like(kc_cpu), torch.full((n,), -1, dtype=torch.int32))
+    empty = torch.tensor([], device="cuda")
+    for slots in (torch.zeros(0, dtype=torch.int32, device="cuda"), None):
+        q, k = qk_norm_rope_store(positions.cuda(), qkv_cpu.cuda(), wq.cuda(), wk.cuda(), 1e-6,
+                                  cache.cuda().unsqueeze(1), empty, empty, slots, hq, hkv, D, return_k=True)
+        torch.cuda.synchronize()
+        assert_close(q, q_want, "warm-up q")
+        assert_close(k, k_want, "warm-up k")
+    with pytest.raises(ValueError):   # one cache allocated, the other not
+        kc = torch.zeros(1, 16, hkv, D, dtype=torch.uint8, device="cuda").view(torch.float8_e4m3fn)
+        qk_norm_rope_store(positions.cuda(), qkv_cpu.cuda(), wq.cuda(), wk.cuda(), 1e-6, cache.cuda().unsqueeze(1),
+                           kc, empty, None, hq, hkv, D)

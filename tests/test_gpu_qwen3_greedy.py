@@ -9,31 +9,41 @@ prompts of 37, 300, 513 and 129 tokens (steps mix decode rows with prefill
 chunks; one chunk has a single token), plain decode steps, and two steps in
 which two sequences carry three speculative drafts (verification rows).
 
-The test fails on any divergence: every predicting row (including each
-speculative verification row) must have the same greedy token in both runs,
-and the generated token sequences must be identical after the last step.
-Rows whose oracle top-2 margin is within the row's observed logit
-deviation are reported (printed), not excused.
+The seeds are a fixed range (0..7 at one and at two layers), not chosen by
+their outcome.  The criterion is fixed in advance by MARGIN_BOUND
+(tests/qwen3_harness.GreedyComparison):
 
-Seeds: the two runs' logits differ by up to ~0.09 (two layers) or ~0.045
-(one layer) -- the fp16 P of the kernels and the bf16 output rounding flip
-single bf16 ulps of some attention outputs, which the second layer's FP8
-re-quantisation of K/V amplifies.  A random-init LM head has top-2 margins
-distributed down to 0, so some seeds contain a numerical tie that either
-implementation could break either way; the seeds below have none (minimum
-top-2 margins 0.057 and 0.049 over their 89 rows on MI355X).
+* every predicting row must give the same greedy token in both runs, unless
+  the oracle's top-2 margin on that row is below MARGIN_BOUND (a numerical
+  tie, which either implementation may break either way) -- a flip at a
+  larger margin fails the test;
+* each run feeds back its own token; where the fed-back row flips at a tie,
+  both runs continue with the oracle's token from that row on
+  (teacher-forced), so every later row is still compared on identical inputs;
+* every row's logits agree within LOGIT_TOL.
+
+How many rows have a margin below the bound is a property of the random-init
+model, not of the kernels (the margins are the oracle run's): with logits of
+standard deviation ≈ 3 over 2,048 tokens, about a fifth of the rows do.  It
+is printed, with the flips.
+
+MARGIN_BOUND is 0.2 logits: more than twice the largest logit deviation
+observed between the two runs (≈ 0.045 at one layer, ≈ 0.09 at two -- the
+kernels' fp16 P and the bf16 output rounding flip single bf16 ulps of some
+attention outputs, and a second layer's FP8 re-quantisation of K/V amplifies
+them).
 """
 import copy
 
 import pytest
-import torch
 
 from gpu_util import announce
-from qwen3_harness import GreedyRunner, Qwen3TinyConfig, hip_model, make_sequences, oracle_model
+from qwen3_harness import GreedyComparison, GreedyRunner, Qwen3TinyConfig, hip_model, make_sequences, oracle_model
 
 # Both models keep bf16 activations and round attention outputs to bf16; a
 # gross attention error moves logits by O(1), far outside this tolerance.
 LOGIT_TOL = dict(atol=0.25, rtol=2e-2)
+MARGIN_BOUND = 0.2
 PROMPTS = [37, 300, 513, 129]
 STEPS = 20
 SPEC_STEPS = {7: {1, 3}, 13: {0, 2}}
@@ -41,8 +51,9 @@ DRAFTS = [7, 1000, 42]
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("layers,seed", [(2, 7), (1, 1)])
-def test_free_running_greedy_sequences_identical(layers, seed):
+@pytest.mark.parametrize("seed", list(range(8)))
+@pytest.mark.parametrize("layers", [1, 2])
+def test_free_running_greedy(layers, seed):
     announce(f"qwen3 greedy (free-running): {layers} layer(s), seed {seed}, 32/8 heads, "
              f"prompts {PROMPTS}, {STEPS} steps, speculative steps {sorted(SPEC_STEPS)}")
     cfg = Qwen3TinyConfig(num_layers=layers, hidden_size=2048, num_heads=32, num_kv_heads=8)
@@ -53,7 +64,7 @@ def test_free_running_greedy_sequences_identical(layers, seed):
     seqs_o = copy.deepcopy(seqs_h)
     run_h = GreedyRunner(hip, cfg.block_size, chunk=256)
     run_o = GreedyRunner(ora, cfg.block_size, chunk=256)
-    worst, min_margin, n_rows, near_ties = 0.0, float("inf"), 0, []
+    cmp = GreedyComparison(MARGIN_BOUND, LOGIT_TOL)
     for step in range(STEPS):
         spec = SPEC_STEPS.get(step, set())
         for sq in (seqs_h, seqs_o):
@@ -63,30 +74,10 @@ def test_free_running_greedy_sequences_identical(layers, seed):
         out_o = run_o.step(seqs_o, spec)
         assert sorted(out_h) == sorted(out_o)
         for i in sorted(out_h):
-            lh, lo = out_h[i].cpu(), out_o[i].cpu()
-            assert lh.shape == lo.shape
-            dev = (lh - lo).abs().max(dim=-1).values
-            worst = max(worst, float(dev.max()))
-            assert torch.allclose(lh, lo, **LOGIT_TOL), \
-                f"step {step} seq {i}: logits differ by up to {float(dev.max())}"
-            top2 = lo.topk(2, dim=-1).values
-            margins = (top2[:, 0] - top2[:, 1]).tolist()
-            th, to = lh.argmax(-1).tolist(), lo.argmax(-1).tolist()
-            for r, (a, b, mg, dv) in enumerate(zip(th, to, margins, dev.tolist())):
-                n_rows += 1
-                min_margin = min(min_margin, mg)
-                if mg <= dv:
-                    near_ties.append((step, i, r, mg, dv))
-                    print(f"[qwen3-greedy] near tie: step {step} seq {i} row {r}: top-2 margin {mg:.4f} "
-                          f"<= |dlogit| {dv:.4f}", flush=True)
-                assert a == b, (f"step {step} seq {i} row {r}: HIP greedy token {a} != oracle {b} "
-                                f"(oracle top-2 margin {mg:.4f}, row |dlogit| {dv:.4f})")
-            # free-running: each run continues with its own greedy token
-            seqs_h[i].tokens.append(th[0])
-            seqs_o[i].tokens.append(to[0])
-    for i, (a, b) in enumerate(zip(seqs_h, seqs_o)):
-        assert a.tokens == b.tokens, f"sequence {i}: generated tokens differ"
-    print(f"[qwen3-greedy] {layers} layer(s), seed {seed}: {n_rows} predicting rows, identical greedy tokens "
-          f"and sequences; max |dlogit| {worst:.4f}; min top-2 margin {min_margin:.4f}; "
-          f"{len(near_ties)} rows with margin <= their |dlogit|", flush=True)
-    assert n_rows >= 80
+            tok = cmp.check(step, i, out_h[i], out_o[i])
+            seqs_h[i].tokens.append(tok)
+            seqs_o[i].tokens.append(tok)
+    print(f"[qwen3-greedy] {layers} layer(s), seed {seed}: {cmp.n_rows} rows compared, max |dlogit| "
+          f"{cmp.worst:.4f}, {cmp.ties} rows with margin < {MARGIN_BOUND}, flips {cmp.flips}, "
+          f"teacher-forced at {cmp.forced}", flush=True)
+    assert cmp.n_rows >= 80
