@@ -221,7 +221,21 @@ def bench_store(wl, steps, warmup, n_src=6):
 
     ms = timed(step, steps, warmup, SECONDARY_WARM_S)
     nbytes = n * hkv * 128 * (2 * 2 + 2) + 4 * n
-    return dict(ms=ms, bytes=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9)
+    # Ceilings for the same traffic: torch's own bf16 -> float8_e4m3fn
+    # conversion of as many contiguous elements (2 B read, 1 B written per
+    # element), and a device-to-device copy moving the same total bytes
+    # (nbytes / 2 read, nbytes / 2 written); n_src sources rotate as above.
+    elems = 2 * n * hkv * 128
+    conv_src = [torch.randn(elems, generator=g, device="cuda").to(torch.bfloat16) for _ in range(n_src)]
+    conv_dst = torch.empty(elems, dtype=torch.float8_e4m3fn, device="cuda")
+    ms_conv = timed(lambda i: conv_dst.copy_(conv_src[i % n_src]), steps, warmup, SECONDARY_WARM_S)
+    half = nbytes // 2 // 16 * 16
+    cp_src = [t.view(torch.uint8)[:half] for t in conv_src]
+    cp_dst = torch.empty(half, dtype=torch.uint8, device="cuda")
+    ms_copy = timed(lambda i: cp_dst.copy_(cp_src[i % n_src]), steps, warmup, SECONDARY_WARM_S)
+    del conv_src, conv_dst, cp_src, cp_dst
+    return dict(ms=ms, bytes=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9, conversion_copy_ms=ms_conv,
+                device_copy_ms=ms_copy, device_copy_bytes=2 * half)
 
 
 def bench_qk_norm_rope(wl, steps, warmup, n_src=6):
@@ -333,10 +347,27 @@ def bench_fp8_linear(M, N, K, steps, warmup, n_weights=2):
     ms_linear = timed(lambda i: fp8_block_linear(x, ws[i % n_weights], w_scale), steps, warmup)
     flops = 2.0 * M * N * K
     weight_bytes = N * K + (N // 128) * (K // 128) * 2
-    return dict(ms=ms_gemm, tflops=flops / (ms_gemm * 1e-3) / 1e12,
-                weight_gbs=weight_bytes / (ms_gemm * 1e-3) / 1e9,
-                quant_us=ms_quant * 1e3, quant_gbs=3.0 * M * K / (ms_quant * 1e-3) / 1e9,
-                linear_us=ms_linear * 1e3, flops=flops, weight_bytes=weight_bytes)
+    res = dict(ms=ms_gemm, tflops=flops / (ms_gemm * 1e-3) / 1e12,
+               weight_gbs=weight_bytes / (ms_gemm * 1e-3) / 1e9,
+               quant_us=ms_quant * 1e3, quant_gbs=3.0 * M * K / (ms_quant * 1e-3) / 1e9,
+               linear_us=ms_linear * 1e3, flops=flops, weight_bytes=weight_bytes)
+    res["hipblaslt_per_tensor_us"] = scaled_mm_us(xq.view(torch.float8_e4m3fn), ws, steps, warmup)
+    return res
+
+
+def scaled_mm_us(xq, ws, steps, warmup):
+    """The same product through torch._scaled_mm (hipBLASLt's FP8 GEMM) with
+    ONE scale per tensor instead of 128 x 128 block scales: a comparison
+    figure for the block-scaled kernel (less work: no per-block promotion).
+    None where torch has no FP8 GEMM for this device."""
+    one = torch.ones((), device="cuda", dtype=torch.float32)
+    try:
+        ms = timed(lambda i: torch._scaled_mm(xq, ws[i % len(ws)].t(), scale_a=one, scale_b=one,
+                                              out_dtype=torch.bfloat16), steps, warmup, warm_s=SECONDARY_WARM_S)
+    except (RuntimeError, TypeError) as e:
+        log(f"torch._scaled_mm unavailable: {e}")
+        return None
+    return round(ms * 1e3, 2)
 
 
 def bench_host_overhead(calls=300):
@@ -380,7 +411,7 @@ def bench_host_overhead(calls=300):
     ws = torch.empty(max(ws_n, 1), dtype=torch.uint8, device="cuda")
     out = torch.empty_like(q)
     args = (out.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), bt.data_ptr(), ctx.data_ptr(), B, hq, hkv, 128,
-            nb_pool, bs, max_nb, SCALE, 0, ws.data_ptr(), ws_n, torch.cuda.current_stream().cuda_stream)
+            nb_pool, bs, max_nb, SCALE, 0, ws.data_ptr(), ws_n, 0, torch.cuda.current_stream().cuda_stream)
     dec = lib.nvamd_fp8_decode_attention
     res["c_abi_decode"] = host_us(lambda: dec(*args))
     # the mixed batch's varlen call: 32 speculative sequences of 5 rows + 3 chunks (64 rows here)
@@ -760,10 +791,19 @@ def main():
         wl = W.qwen3_8b_prefill()
         res = bench_store(wl, max(args.steps, 20), max(args.warmup, 5))
         log(f"store: {res['ms'] * 1e3:.1f} us/step, {res['gbs']:.1f} GB/s")
+        log(f"store ceilings: torch bf16->fp8 conversion of as many elements {res['conversion_copy_ms'] * 1e3:.1f} us; "
+            f"device copy of the same total bytes {res['device_copy_ms'] * 1e3:.1f} us")
         extra["store"] = dict(workload=wl.name + " new tokens (8192 x 8 kv heads, strided K/V views of qkv)",
                               ms_per_step=round(res["ms"], 5), gbs=round(res["gbs"], 2),
                               frac_hbm_peak=round(res["gbs"] / HBM_PEAK_GBS, 4), algorithmic_bytes_per_step=res["bytes"],
-                              kernels="kv_store_fp8_kernel")
+                              kernels="kv_store_fp8_kernel",
+                              ceilings=dict(
+                                  conversion_copy_ms=round(res["conversion_copy_ms"], 5),
+                                  conversion_copy="torch bf16 -> float8_e4m3fn copy_ of the same 2 x 8192 x 8 x 128 "
+                                                  "contiguous elements (same read and write bytes, no slot ids)",
+                                  device_copy_ms=round(res["device_copy_ms"], 5),
+                                  device_copy_gbs=round(res["device_copy_bytes"] / (res["device_copy_ms"] * 1e-3) / 1e9, 2),
+                                  device_copy="torch uint8 copy_ moving the same total bytes (half read, half written)"))
         torch.cuda.empty_cache()
 
     if want("store"):
@@ -824,23 +864,32 @@ def main():
         # Qwen3-8B FP8 checkpoints: the qkv projection of a 16 x 512-token
         # prefill step (MFMA-bound) and the gate/up projection of the mixed
         # batch's 192 decode rows (weight-streaming, HBM-bound)
-        big = bench_fp8_linear(8192, 6144, 4096, max(args.steps // 2, 10), max(args.warmup // 2, 3))
-        small = bench_fp8_linear(192, 24576, 4096, max(args.steps, 20), max(args.warmup, 5))
-        log(f"fp8 linear: qkv M=8192 {big['ms'] * 1e3:.1f} us ({big['tflops']:.0f} TFLOP/s); "
-            f"gate_up M=192 {small['ms'] * 1e3:.1f} us ({small['weight_gbs']:.0f} GB/s of weights)")
+        # Qwen3-8B FP8 checkpoints at the 16 x 512-token prefill step (qkv,
+        # gate/up and down projections, MFMA-bound) and at the mixed batch's
+        # 192 decode rows (weight-streaming, HBM-bound)
+        lin = {}
+        for name, (M, N, K) in (("prefill_qkv", (8192, 6144, 4096)), ("prefill_gate_up", (8192, 24576, 4096)),
+                                ("prefill_down", (8192, 4096, 12288)), ("decode_qkv", (192, 6144, 4096)),
+                                ("decode_gate_up", (192, 24576, 4096)), ("decode_down", (192, 4096, 12288))):
+            big = M >= 1024
+            r = bench_fp8_linear(M, N, K, max(args.steps // 2, 10) if big else max(args.steps, 20),
+                                 max(args.warmup // 2, 3) if big else max(args.warmup, 5))
+            e = dict(shape=f"M={M} tokens, N={N}, K={K}", ms_per_step=round(r["ms"], 5),
+                     tflops=round(r["tflops"], 1), frac_fp8_peak=round(r["tflops"] / FP8_PEAK_TFLOPS, 4),
+                     algorithmic_flops=r["flops"], quant_us=round(r["quant_us"], 2),
+                     quant_gbs=round(r["quant_gbs"], 1), fp8_block_linear_us=round(r["linear_us"], 2),
+                     hipblaslt_per_tensor_us=r["hipblaslt_per_tensor_us"])
+            if not big:
+                e.update(weight_gbs=round(r["weight_gbs"], 1), frac_hbm_peak=round(r["weight_gbs"] / HBM_PEAK_GBS, 4),
+                         algorithmic_bytes=r["weight_bytes"])
+            lin[name] = e
+            log(f"fp8 linear {name} M={M} N={N} K={K}: {r['ms'] * 1e3:.1f} us ({r['tflops']:.0f} TFLOP/s"
+                + ("" if big else f", {r['weight_gbs']:.0f} GB/s of weights")
+                + f"); hipBLASLt per-tensor {r['hipblaslt_per_tensor_us']} us")
         extra["fp8_linear"] = dict(
             workload="FP8 block-scaled linear (128x128 weight blocks), Qwen3-8B shapes",
-            kernels="block_gemm_kernel (act_quant_kernel timed separately)",
-            prefill_qkv=dict(shape="M=8192 tokens, N=6144, K=4096", ms_per_step=round(big["ms"], 5),
-                             tflops=round(big["tflops"], 1), frac_fp8_peak=round(big["tflops"] / FP8_PEAK_TFLOPS, 4),
-                             algorithmic_flops=big["flops"], quant_us=round(big["quant_us"], 2),
-                             quant_gbs=round(big["quant_gbs"], 1), fp8_block_linear_us=round(big["linear_us"], 2)),
-            decode_gate_up=dict(shape="M=192 tokens, N=24576, K=4096", ms_per_step=round(small["ms"], 5),
-                                weight_gbs=round(small["weight_gbs"], 1),
-                                frac_hbm_peak=round(small["weight_gbs"] / HBM_PEAK_GBS, 4),
-                                algorithmic_bytes=small["weight_bytes"], tflops=round(small["tflops"], 1),
-                                quant_us=round(small["quant_us"], 2),
-                                fp8_block_linear_us=round(small["linear_us"], 2)))
+            kernels="block_gemm_kernel (act_quant_kernel timed separately); hipblaslt_per_tensor_us: "
+                    "torch._scaled_mm with one scale per tensor, same operands", **lin)
         if not args.no_cpu_baseline:
             log("cpu baseline (oracle) for the FP8 linear")
             extra["fp8_linear"]["cpu_baseline"] = cpu_baseline_fp8_linear(6144, 4096)

@@ -21,8 +21,11 @@
  *     allocates memory or synchronises; every kernel is enqueued on `stream`
  *     (a hipStream_t, NULL = default stream), so the calls may be captured
  *     into a HIP graph.
- *   - bf16 tensors are passed as raw 16-bit storage; FP8 tensors hold OCP
- *     E4M3FN bytes (torch.float8_e4m3fn).  Integer metadata is int32.
+ *   - bf16 / fp16 tensors are passed as raw 16-bit storage, their type named
+ *     by a dtype argument (NVAMD_DTYPE_BF16 or NVAMD_DTYPE_F16; the
+ *     reference's Triton kernels take the type of the tensors they are
+ *     given); FP8 tensors hold OCP E4M3FN bytes (torch.float8_e4m3fn).
+ *     Integer metadata is int32.
  *   - head_dim must be 128 for the attention kernels; block_size must be a
  *     positive multiple of 16 (the reference's kvcache_block_size rule,
  *     nanovllm/config.py:30).
@@ -50,8 +53,12 @@ extern "C" {
 #define NVAMD_ERR_WORKSPACE 3
 #define NVAMD_ERR_LAUNCH 4
 
+/* Element types of 16-bit float tensors. */
+#define NVAMD_DTYPE_BF16 0
+#define NVAMD_DTYPE_F16 1
+
 /* ABI version of this header and nvamd_fp8_linear.h (bumped on any signature change). */
-#define NVAMD_ABI_VERSION 5
+#define NVAMD_ABI_VERSION 6
 int32_t nvamd_abi_version(void);
 
 /* Description of the last error on the calling thread ("" if none). */
@@ -61,8 +68,9 @@ const char* nvamd_last_error(void);
  * FP8 KV-cache store / quantise.  Replaces store_kvcache_kernel
  * (nanovllm/layers/attention.py:11-31, launched at :40).
  *
- * key/value: bf16, num_tokens rows of num_kv_heads*head_dim contiguous
- *   elements (strides (key_stride0, head_dim, 1)), row stride in elements.
+ * key/value: kv_dtype (bf16 or fp16), num_tokens rows of num_kv_heads*head_dim
+ *   contiguous elements (strides (key_stride0, head_dim, 1)), row stride in
+ *   elements.
  * k_cache/v_cache: E4M3FN [num_slots, num_kv_heads*head_dim] contiguous
  *   (num_slots = num_blocks*block_size).
  * slot_mapping: int32[num_tokens]; -1 skips the row (attention.py:24).
@@ -74,7 +82,7 @@ int32_t nvamd_store_kvcache(const void* key, int64_t key_stride0,
                             void* k_cache, void* v_cache,
                             const int32_t* slot_mapping, int64_t num_tokens,
                             int32_t num_kv_heads, int32_t head_dim, int64_t num_slots,
-                            void* stream);
+                            int32_t kv_dtype, void* stream);
 
 /*
  * Fused q/k RMSNorm + rotary embedding + FP8 KV store of one attention
@@ -152,15 +160,17 @@ int64_t nvamd_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t n
  * fp8_paged_attention_decode_kernel (nanovllm/kernels/fp8_attention.py:88-171,
  * launched at :196-206).
  *
- * out, q: bf16 [batch, num_heads, head_dim] contiguous (q may have more rows;
- *   only the first `batch` are used, as in the reference where batch comes
- *   from block_tables.shape[0]).
+ * out, q: qo_dtype (bf16 or fp16) [batch, num_heads, head_dim] contiguous (q
+ *   may have more rows; only the first `batch` are used, as in the reference
+ *   where batch comes from block_tables.shape[0]).  out has q's type
+ *   (empty_like(q), fp8_attention.py:193).
  * k_cache/v_cache: E4M3FN [num_blocks, block_size, num_kv_heads, head_dim].
  * block_tables: int32 [batch, max_num_blocks] row-major; entries past
  *   ceil(context_lens[b]/block_size) are never read.
  * context_lens: int32 [batch].  A row with context 0 is written as zeros
  *   (the reference produces NaN there).
- * out = bf16(fp16(softmax(scale * q.K^T) . V)), fp32 accumulation.
+ * out = fp16(softmax(scale * q.K^T) . V), fp32 accumulation, stored as fp16,
+ *   or for bf16 as bf16(fp16(.)) (the reference casts to fp16, :169).
  * part_tokens: split-KV partition length (multiple of 256, at most
  *   63 blocks) or 0 = automatic.
  */
@@ -171,7 +181,7 @@ int32_t nvamd_fp8_decode_attention(void* out, const void* q,
                                    int32_t head_dim, int64_t num_blocks, int32_t block_size,
                                    int32_t max_num_blocks, float softmax_scale,
                                    int32_t part_tokens, void* workspace, int64_t workspace_bytes,
-                                   void* stream);
+                                   int32_t qo_dtype, void* stream);
 
 /*
  * Paged decode that allocates nothing and takes no workspace.  This entry
@@ -196,7 +206,8 @@ int32_t nvamd_fp8_decode_attention_noalloc(void* out, const void* q,
                                            const int32_t* block_tables, const int32_t* context_lens,
                                            int32_t batch, int32_t num_heads, int32_t num_kv_heads,
                                            int32_t head_dim, int64_t num_blocks, int32_t block_size,
-                                           int32_t max_num_blocks, float softmax_scale, void* stream);
+                                           int32_t max_num_blocks, float softmax_scale, int32_t qo_dtype,
+                                           void* stream);
 
 /* Workspace needed by nvamd_fp8_prefill_attention.  kv_cap is the static
  * upper bound of keys per sequence: max_num_blocks*block_size for the paged
@@ -213,7 +224,8 @@ int64_t nvamd_prefill_workspace_bytes(int64_t num_tokens, int32_t num_seqs, int3
  * fp8_paged_attention_prefill_kernel (nanovllm/kernels/fp8_attention.py:209-312,
  * launched at :341-352).
  *
- * q, out: bf16 [num_tokens, num_heads, head_dim] contiguous.
+ * q, out: qo_dtype (bf16 or fp16) [num_tokens, num_heads, head_dim]
+ *   contiguous; out rounded as for decode.
  * Paged layout (block_tables != NULL): k/v are E4M3FN caches
  *   [num_kv_rows/block_size, block_size, num_kv_heads, head_dim] and
  *   block_tables is int32 [num_seqs, max_num_blocks].
@@ -238,7 +250,8 @@ int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, con
                                     int32_t block_size, int32_t max_num_blocks,
                                     int32_t max_seqlen_q, int32_t max_seqlen_k,
                                     float softmax_scale, int32_t part_tokens,
-                                    void* workspace, int64_t workspace_bytes, void* stream);
+                                    void* workspace, int64_t workspace_bytes, int32_t qo_dtype,
+                                    void* stream);
 
 #ifdef __cplusplus
 }

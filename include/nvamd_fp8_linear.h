@@ -28,9 +28,6 @@
 extern "C" {
 #endif
 
-#define NVAMD_DTYPE_BF16 0
-#define NVAMD_DTYPE_F16 1
-
 /*
  * Per-token, per-128-column dynamic quantisation of the activations.
  * Replaces fp8_dyn_quant_kernel (nanovllm/kernels/fp8_linear.py:11-31).

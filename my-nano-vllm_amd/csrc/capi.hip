@@ -158,6 +158,12 @@ void set_partials(nvamd::MqParams& p, void* workspace) {
   p.part_ml = p.part_acc ? p.part_acc + n * kHeadDim : nullptr;
 }
 
+int32_t check_qo_dtype(const char* fn, int32_t qo_dtype) {
+  if (qo_dtype != NVAMD_DTYPE_BF16 && qo_dtype != NVAMD_DTYPE_F16)
+    return fail(NVAMD_ERR_UNSUPPORTED, "%s: qo_dtype must be bf16 or fp16 (got %d)", fn, qo_dtype);
+  return NVAMD_OK;
+}
+
 int32_t check_heads(const char* fn, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim) {
   if (head_dim != kHeadDim)
     return fail(NVAMD_ERR_UNSUPPORTED, "%s: head_dim must be %d (got %d)", fn, kHeadDim, head_dim);
@@ -214,7 +220,9 @@ const char* nvamd_last_error(void) { return g_last_error.c_str(); }
 int32_t nvamd_store_kvcache(const void* key, int64_t key_stride0, const void* value,
                             int64_t value_stride0, void* k_cache, void* v_cache,
                             const int32_t* slot_mapping, int64_t num_tokens, int32_t num_kv_heads,
-                            int32_t head_dim, int64_t num_slots, void* stream) {
+                            int32_t head_dim, int64_t num_slots, int32_t kv_dtype, void* stream) {
+  if (kv_dtype != NVAMD_DTYPE_BF16 && kv_dtype != NVAMD_DTYPE_F16)
+    return fail(NVAMD_ERR_UNSUPPORTED, "store_kvcache: kv_dtype must be bf16 or fp16 (got %d)", kv_dtype);
   if (num_tokens < 0 || num_kv_heads <= 0 || head_dim <= 0 || num_slots < 0)
     return fail(NVAMD_ERR_INVALID_ARGUMENT, "store_kvcache: bad sizes (N=%lld Hkv=%d D=%d slots=%lld)",
                 (long long)num_tokens, num_kv_heads, head_dim, (long long)num_slots);
@@ -227,7 +235,7 @@ int32_t nvamd_store_kvcache(const void* key, int64_t key_stride0, const void* va
                    ((uintptr_t)k_cache % 16 == 0) && ((uintptr_t)v_cache % 16 == 0);
   return launch_status(nvamd::launch_kv_store(key, key_stride0, value, value_stride0, k_cache, v_cache,
                                               slot_mapping, num_tokens, row, num_slots, vec,
-                                              (hipStream_t)stream),
+                                              kv_dtype == NVAMD_DTYPE_F16, (hipStream_t)stream),
                        "store_kvcache");
 }
 
@@ -471,8 +479,10 @@ int32_t decode_attention(const char* fn, void* out, const void* q, const void* k
                          const int32_t* block_tables, const int32_t* context_lens, int32_t batch,
                          int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int64_t num_blocks,
                          int32_t block_size, int32_t max_num_blocks, float softmax_scale, int32_t part_tokens,
-                         void* workspace, int64_t workspace_bytes, void* stream, bool lib_scratch) {
+                         void* workspace, int64_t workspace_bytes, int32_t qo_dtype, void* stream,
+                         bool lib_scratch) {
   if (int32_t e = check_heads(fn, num_heads, num_kv_heads, head_dim)) return e;
+  if (int32_t e = check_qo_dtype(fn, qo_dtype)) return e;
   if (!(softmax_scale > 0.f) || !std::isfinite(softmax_scale))
     return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: softmax_scale must be positive and finite", fn);
   if (batch < 0 || num_blocks < 0 || max_num_blocks < 0)
@@ -522,6 +532,7 @@ int32_t decode_attention(const char* fn, void* out, const void* q, const void* k
   const int64_t kv_cap = (int64_t)max_num_blocks * block_size;
   p.mq_max_q = 1;
   p.scale_log2 = softmax_scale * 1.4426950408889634f;
+  p.out_f16 = qo_dtype == NVAMD_DTYPE_F16;
   const int ncb = (G + 15) / 16;
   if (use_stream_k(batch, num_kv_heads, part_tokens)) {
     const int64_t need = stream_k_bytes(batch, num_kv_heads, G, G, false);
@@ -558,20 +569,21 @@ int32_t nvamd_fp8_decode_attention(void* out, const void* q, const void* k_cache
                                    int32_t batch, int32_t num_heads, int32_t num_kv_heads,
                                    int32_t head_dim, int64_t num_blocks, int32_t block_size,
                                    int32_t max_num_blocks, float softmax_scale, int32_t part_tokens,
-                                   void* workspace, int64_t workspace_bytes, void* stream) {
+                                   void* workspace, int64_t workspace_bytes, int32_t qo_dtype, void* stream) {
   return decode_attention("fp8_decode_attention", out, q, k_cache, v_cache, block_tables, context_lens, batch,
                           num_heads, num_kv_heads, head_dim, num_blocks, block_size, max_num_blocks, softmax_scale,
-                          part_tokens, workspace, workspace_bytes, stream, false);
+                          part_tokens, workspace, workspace_bytes, qo_dtype, stream, false);
 }
 
 int32_t nvamd_fp8_decode_attention_noalloc(void* out, const void* q, const void* k_cache, const void* v_cache,
                                            const int32_t* block_tables, const int32_t* context_lens,
                                            int32_t batch, int32_t num_heads, int32_t num_kv_heads,
                                            int32_t head_dim, int64_t num_blocks, int32_t block_size,
-                                           int32_t max_num_blocks, float softmax_scale, void* stream) {
+                                           int32_t max_num_blocks, float softmax_scale, int32_t qo_dtype,
+                                           void* stream) {
   return decode_attention("fp8_decode_attention_noalloc", out, q, k_cache, v_cache, block_tables, context_lens,
                           batch, num_heads, num_kv_heads, head_dim, num_blocks, block_size, max_num_blocks,
-                          softmax_scale, 0, nullptr, 0, stream, true);
+                          softmax_scale, 0, nullptr, 0, qo_dtype, stream, true);
 }
 
 int64_t nvamd_prefill_workspace_bytes(int64_t num_tokens, int32_t num_seqs, int32_t num_heads,
@@ -595,10 +607,11 @@ int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, con
                                     int64_t num_kv_rows, int32_t block_size, int32_t max_num_blocks,
                                     int32_t max_seqlen_q, int32_t max_seqlen_k, float softmax_scale,
                                     int32_t part_tokens, void* workspace, int64_t workspace_bytes,
-                                    void* stream) {
+                                    int32_t qo_dtype, void* stream) {
   static const char* fn = "fp8_prefill_attention";
   (void)max_seqlen_k;
   if (int32_t e = check_heads(fn, num_heads, num_kv_heads, head_dim)) return e;
+  if (int32_t e = check_qo_dtype(fn, qo_dtype)) return e;
   if (!(softmax_scale > 0.f) || !std::isfinite(softmax_scale))
     return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: softmax_scale must be positive and finite", fn);
   if (num_tokens < 0 || num_seqs < 0 || num_kv_rows < 0 || max_seqlen_q < 0)
@@ -662,6 +675,7 @@ int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, con
   mp.max_parts = (int)ceil_div(kv_cap, part);
   mp.mq_max_q = std::min(mq_max_q, max_seqlen_q);
   mp.scale_log2 = softmax_scale * 1.4426950408889634f;
+  mp.out_f16 = qo_dtype == NVAMD_DTYPE_F16;
   const int ncb = (G * mp.mq_max_q + 15) / 16;
   const bool all_short = max_seqlen_q <= mq_max_q;
   if (sk) {
@@ -709,6 +723,7 @@ int32_t nvamd_fp8_prefill_attention(void* out, const void* q, const void* k, con
   pp.blk_magic = (uint32_t)(((1u << 31) - 1u) / (uint32_t)(pp.block_size / 16) + 1u);
   pp.mq_max_q = mq_max_q;
   pp.scale_log2 = softmax_scale * 1.4426950408889634f;
+  pp.out_f16 = qo_dtype == NVAMD_DTYPE_F16;
   char* schedule = static_cast<char*>(workspace) + align_up(partials);
   if (layout.records > 0x7fffffff / ((int64_t)num_kv_heads * pp.n_hgroups))
     return fail(NVAMD_ERR_UNSUPPORTED, "%s: too many prefill work items", fn);

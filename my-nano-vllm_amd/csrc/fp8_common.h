@@ -6,7 +6,8 @@
 //     even; magnitudes beyond 448 saturate to +-448, NaN stays NaN.
 //   * FP8 -> bf16 is exact (every E4M3FN value is a bf16 value), so the MFMA
 //     operands carry the cache values unchanged.
-//   * Outputs are written as bf16(fp16(x)), the reference's double rounding.
+//   * Outputs are written as bf16(fp16(x)) for bf16 queries, the reference's
+//     double rounding, and as fp16(x) for fp16 queries (out = empty_like(q)).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -119,6 +120,61 @@ __device__ __forceinline__ uint32_t out_round_bf16_bits(float x) {
   if ((u & 0x7F800000u) == 0x7F800000u) return u >> 16;  // inf / NaN keep their class
   u += 0x7FFFu + ((u >> 16) & 1u);
   return u >> 16;
+}
+
+// fp16 output (q and out fp16, empty_like(q) in the reference): fp32 -> fp16
+// (RNE) only.  Returns the fp16 bits.
+__device__ __forceinline__ uint32_t out_round_f16_bits(float x) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+}
+
+// ---------------------------------------------------------------------------
+// The query / output element type of the attention kernels
+// ---------------------------------------------------------------------------
+// F16 = false: bf16 q, S = K . Q^T on the bf16 MFMAs with K converted to bf16;
+// out = bf16(fp16(x)).  F16 = true: fp16 q, the fp16 MFMAs with K converted to
+// fp16; out = fp16(x).  Both conversions of the FP8 cache are exact, so in
+// either case S is the fp32-accumulated product of the exact q and K values.
+template <bool F16>
+struct QkType;
+
+template <>
+struct QkType<false> {
+  using V8 = bf16x8;
+  static __device__ __forceinline__ V8 from_bits(u32x4 t) { return __builtin_bit_cast(bf16x8, t); }
+  template <bool HI>
+  static __device__ __forceinline__ uint32_t k2(uint32_t w) {  // two E4M3FN bytes -> two elements
+    return fp8x2_to_bf16x2<HI>(w);
+  }
+  static __device__ __forceinline__ f32x4 mfma16(V8 a, V8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x16 mfma32(V8 a, V8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t out_bits(float x) { return out_round_bf16_bits(x); }
+};
+
+template <>
+struct QkType<true> {
+  using V8 = f16x8;
+  static __device__ __forceinline__ V8 from_bits(u32x4 t) { return __builtin_bit_cast(f16x8, t); }
+  template <bool HI>
+  static __device__ __forceinline__ uint32_t k2(uint32_t w) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, HI));
+  }
+  static __device__ __forceinline__ f32x4 mfma16(V8 a, V8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x16 mfma32(V8 a, V8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t out_bits(float x) { return out_round_f16_bits(x); }
+};
+
+// Output rounding chosen at run time (merge passes shared by both types).
+__device__ __forceinline__ uint32_t out_bits_rt(float x, bool f16) {
+  return f16 ? out_round_f16_bits(x) : out_round_bf16_bits(x);
 }
 
 // ---------------------------------------------------------------------------

@@ -8,7 +8,7 @@ namespace nvamd {
 
 // Paged decode / short-query attention (split-KV).
 struct MqParams {
-  const uint16_t* q;            // bf16 [q_rows, Hq, 128]
+  const uint16_t* q;            // bf16 or fp16 (out_f16) [q_rows, Hq, 128]
   const uint8_t* k;             // FP8: paged [P, bs, Hkv, 128] or contiguous [Nk, Hkv, 128]
   const uint8_t* v;
   const int32_t* block_tables;  // [num_seqs, bt_stride]; nullptr = contiguous layout
@@ -16,7 +16,7 @@ struct MqParams {
   const int32_t* context_lens;  // decode mode: [num_seqs]
   const int32_t* cu_q;          // varlen mode: [num_seqs + 1] (nullptr in decode mode)
   const int32_t* cu_k;
-  uint16_t* out;                // bf16 [q_rows, Hq, 128]
+  uint16_t* out;                // [q_rows, Hq, 128], the type of q
   float* part_acc;              // [q_rows * Hq, max_parts, 128]
   float* part_ml;               // [q_rows * Hq, max_parts, 2]
   int64_t q_rows;               // rows of q / out
@@ -27,6 +27,7 @@ struct MqParams {
   int part_tokens, max_parts;
   int mq_max_q;                 // varlen mode: only sequences with 1 <= Lq <= mq_max_q
   float scale_log2;
+  int out_f16;                  // q and out are fp16 (else bf16)
   // Balanced decode (stream-K over KV stages), see decode_sk_kernel.
   float* sk_part;               // [sk_wgs, 2, sk_heads, sk_cols, kSkSlotFloats] partials (see kSkSlotFloats)
   int32_t* sk_prefix;           // [num_seqs + 1] stages per kv-head group before each sequence
@@ -69,6 +70,7 @@ struct PrefillParams {
   uint32_t blk_magic;  // ceil(2^31 / (block_size / 16)): block of key kv = umulhi(2 * (kv >> 4), blk_magic)
   int mq_max_q;   // sequences with Lq <= mq_max_q are left to the short-query kernel
   float scale_log2;
+  int out_f16;    // q and out are fp16 (else bf16)
   // Work list and split key ranges (see prefill_schedule): a call with fewer
   // items than a round of workgroups splits its long items' tiles into
   // pieces whose partial results the item's last piece merges.
@@ -153,7 +155,7 @@ hipError_t launch_fp8_block_gemm(const Fp8GemmParams& p, int config, bool f16_ou
 hipError_t launch_kv_store(const void* key, int64_t key_stride, const void* value,
                            int64_t value_stride, void* k_cache, void* v_cache,
                            const int32_t* slot_mapping, int64_t num_tokens, int row_elems,
-                           int64_t num_slots, bool vec, hipStream_t stream);
+                           int64_t num_slots, bool vec, bool f16, hipStream_t stream);
 
 hipError_t launch_paged_mq(const MqParams& p, int ncb, hipStream_t stream);
 // Persistent workgroups the balanced decode kernel keeps resident per CU.

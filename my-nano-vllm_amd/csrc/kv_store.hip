@@ -1,9 +1,10 @@
 // FP8 E4M3FN KV-cache store / quantise for gfx950.
 //
 // Replaces store_kvcache_kernel (nanovllm/layers/attention.py:11-31): for
-// every token i with slot_mapping[i] != -1, the D = Hkv*head_dim bf16 values of
-// key[i] and value[i] are rounded to E4M3FN and written to
-// cache[slot*D : slot*D + D].
+// every token i with slot_mapping[i] != -1, the D = Hkv*head_dim bf16 (or fp16)
+// values of key[i] and value[i] are rounded to E4M3FN and written to
+// cache[slot*D : slot*D + D].  Both 16-bit types widen to fp32 exactly, so the
+// one RNE, saturating fp32 -> E4M3FN conversion rounds the value itself.
 //
 // Design: purely HBM-bound (2 B read + 1 B written per element).  A lane
 // converts 16 consecutive elements of one row at a time: two 16-byte loads,
@@ -20,17 +21,28 @@
 
 namespace nvamd {
 
-// 16 bf16 (two dwords x 4) -> 16 E4M3FN bytes (RNE, satfinite)
+// One 16-bit element (bf16, or fp16 with F16) -> fp32, exact.
+template <bool F16>
+__device__ __forceinline__ float h16_to_f32(uint32_t bits16) {
+  if constexpr (F16) return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+  else return bf16_bits_to_f32(bits16);
+}
+
+// Four 16-bit elements (two dwords) -> four E4M3FN bytes (RNE, satfinite).
+template <bool F16>
+__device__ __forceinline__ uint32_t quantize4(uint32_t lo, uint32_t hi) {
+  return f32x4_to_fp8x4(h16_to_f32<F16>(lo & 0xFFFFu), h16_to_f32<F16>(lo >> 16), h16_to_f32<F16>(hi & 0xFFFFu),
+                        h16_to_f32<F16>(hi >> 16));
+}
+
+// 16 elements (two dwords x 4) -> 16 E4M3FN bytes (RNE, satfinite)
+template <bool F16>
 __device__ __forceinline__ u32x4 quantize16(u32x4 a, u32x4 b) {
   u32x4 o;
-  o.x = f32x4_to_fp8x4(bf16_bits_to_f32(a.x & 0xFFFFu), bf16_bits_to_f32(a.x >> 16),
-                       bf16_bits_to_f32(a.y & 0xFFFFu), bf16_bits_to_f32(a.y >> 16));
-  o.y = f32x4_to_fp8x4(bf16_bits_to_f32(a.z & 0xFFFFu), bf16_bits_to_f32(a.z >> 16),
-                       bf16_bits_to_f32(a.w & 0xFFFFu), bf16_bits_to_f32(a.w >> 16));
-  o.z = f32x4_to_fp8x4(bf16_bits_to_f32(b.x & 0xFFFFu), bf16_bits_to_f32(b.x >> 16),
-                       bf16_bits_to_f32(b.y & 0xFFFFu), bf16_bits_to_f32(b.y >> 16));
-  o.w = f32x4_to_fp8x4(bf16_bits_to_f32(b.z & 0xFFFFu), bf16_bits_to_f32(b.z >> 16),
-                       bf16_bits_to_f32(b.w & 0xFFFFu), bf16_bits_to_f32(b.w >> 16));
+  o.x = quantize4<F16>(a.x, a.y);
+  o.y = quantize4<F16>(a.z, a.w);
+  o.z = quantize4<F16>(b.x, b.y);
+  o.w = quantize4<F16>(b.z, b.w);
   return o;
 }
 
@@ -40,6 +52,7 @@ __device__ __forceinline__ u32x4 quantize16(u32x4 a, u32x4 b) {
 // lane has twice the bytes in flight of a one-chunk lane and half the
 // index arithmetic per byte.  Row r of the launch is token r / 2, K (even)
 // or V (odd).
+template <bool F16>
 __global__ __launch_bounds__(256) void kv_store_fp8_pair_kernel(
     const uint16_t* __restrict__ key, int64_t key_stride, const uint16_t* __restrict__ value, int64_t value_stride,
     uint8_t* __restrict__ k_cache, uint8_t* __restrict__ v_cache, const int32_t* __restrict__ slot_mapping,
@@ -62,12 +75,13 @@ __global__ __launch_bounds__(256) void kv_store_fp8_pair_kernel(
     b[j] = *reinterpret_cast<const u32x4*>(src + e + 8);
   }
 #pragma unroll
-  for (int j = 0; j < 2; ++j) *reinterpret_cast<u32x4*>(dst + 16 * (c0 + j * lanes_per_row)) = quantize16(a[j], b[j]);
+  for (int j = 0; j < 2; ++j)
+    *reinterpret_cast<u32x4*>(dst + 16 * (c0 + j * lanes_per_row)) = quantize16<F16>(a[j], b[j]);
 }
 
 // VEC: rows are 16-byte aligned and D % 16 == 0 (the normal case: K/V are
 // views of the fused qkv projection); otherwise one element per lane-step.
-template <bool VEC>
+template <bool VEC, bool F16>
 __global__ __launch_bounds__(256) void kv_store_fp8_kernel(
     const uint16_t* __restrict__ key, int64_t key_stride,
     const uint16_t* __restrict__ value, int64_t value_stride,
@@ -93,22 +107,23 @@ __global__ __launch_bounds__(256) void kv_store_fp8_kernel(
   if constexpr (VEC) {
     const u32x4 a = *reinterpret_cast<const u32x4*>(src);
     const u32x4 b = *reinterpret_cast<const u32x4*>(src + 8);
-    *reinterpret_cast<u32x4*>(dst) = quantize16(a, b);
+    *reinterpret_cast<u32x4*>(dst) = quantize16<F16>(a, b);
   } else {
-    const float f = bf16_bits_to_f32(*src);
+    const float f = h16_to_f32<F16>(*src);
     const int w = __builtin_amdgcn_cvt_pk_fp8_f32(e4m3_satfinite(f), 0.0f, 0, false);
     *dst = (uint8_t)(w & 0xFF);
   }
 }
 
-hipError_t launch_kv_store(const void* key, int64_t key_stride, const void* value,
-                           int64_t value_stride, void* k_cache, void* v_cache,
-                           const int32_t* slot_mapping, int64_t num_tokens, int row_elems,
-                           int64_t num_slots, bool vec, hipStream_t stream) {
-  if (num_tokens == 0) return hipSuccess;
+namespace {
+
+template <bool F16>
+hipError_t launch_kv_store_t(const void* key, int64_t key_stride, const void* value, int64_t value_stride,
+                             void* k_cache, void* v_cache, const int32_t* slot_mapping, int64_t num_tokens,
+                             int row_elems, int64_t num_slots, bool vec, hipStream_t stream) {
   if (vec && row_elems % 32 == 0 && num_tokens * 2 * (row_elems / 32) + 255 < 0x7fffffff) {
     const int64_t threads = num_tokens * 2 * (row_elems / 32);
-    hipLaunchKernelGGL(kv_store_fp8_pair_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
+    hipLaunchKernelGGL(kv_store_fp8_pair_kernel<F16>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
                        (const uint16_t*)key, key_stride, (const uint16_t*)value, value_stride, (uint8_t*)k_cache,
                        (uint8_t*)v_cache, slot_mapping, (int)num_tokens, row_elems, num_slots);
     return hipGetLastError();
@@ -117,17 +132,30 @@ hipError_t launch_kv_store(const void* key, int64_t key_stride, const void* valu
   const int64_t total = num_tokens * 2 * (row_elems / per_lane);
   const int64_t blocks = (total + 255) / 256;
   if (vec) {
-    hipLaunchKernelGGL(kv_store_fp8_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream,
+    hipLaunchKernelGGL((kv_store_fp8_kernel<true, F16>), dim3((unsigned)blocks), dim3(256), 0, stream,
                        (const uint16_t*)key, key_stride, (const uint16_t*)value, value_stride,
                        (uint8_t*)k_cache, (uint8_t*)v_cache, slot_mapping, num_tokens, row_elems,
                        num_slots);
   } else {
-    hipLaunchKernelGGL(kv_store_fp8_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream,
+    hipLaunchKernelGGL((kv_store_fp8_kernel<false, F16>), dim3((unsigned)blocks), dim3(256), 0, stream,
                        (const uint16_t*)key, key_stride, (const uint16_t*)value, value_stride,
                        (uint8_t*)k_cache, (uint8_t*)v_cache, slot_mapping, num_tokens, row_elems,
                        num_slots);
   }
   return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_kv_store(const void* key, int64_t key_stride, const void* value,
+                           int64_t value_stride, void* k_cache, void* v_cache,
+                           const int32_t* slot_mapping, int64_t num_tokens, int row_elems,
+                           int64_t num_slots, bool vec, bool f16, hipStream_t stream) {
+  if (num_tokens == 0) return hipSuccess;
+  return f16 ? launch_kv_store_t<true>(key, key_stride, value, value_stride, k_cache, v_cache, slot_mapping,
+                                       num_tokens, row_elems, num_slots, vec, stream)
+             : launch_kv_store_t<false>(key, key_stride, value, value_stride, k_cache, v_cache, slot_mapping,
+                                        num_tokens, row_elems, num_slots, vec, stream);
 }
 
 }  // namespace nvamd

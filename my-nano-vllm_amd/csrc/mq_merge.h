@@ -66,7 +66,8 @@ __device__ __forceinline__ void merge_partitions(const MqParams& p, int64_t rh, 
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) L += shfl_xor_f32(L, off);
   const float inv = (L > 0.f) ? 1.0f / L : 0.f;
-  const uint32_t w = out_round_bf16_bits(o0 * inv) | (out_round_bf16_bits(o1 * inv) << 16);
+  const bool f16 = p.out_f16 != 0;
+  const uint32_t w = out_bits_rt(o0 * inv, f16) | (out_bits_rt(o1 * inv, f16) << 16);
   *reinterpret_cast<uint32_t*>(p.out + rh * kHeadDim + 2 * lane) = w;
 }
 
@@ -251,7 +252,8 @@ __device__ __forceinline__ void sk_merge_one(const MqParams& p, int b, int idx, 
     }
   }
   const float inv = (Lsum > 0.f) ? 1.0f / Lsum : 0.f;
-  out[lane] = out_round_bf16_bits(o0 * inv) | (out_round_bf16_bits(o1 * inv) << 16);
+  const bool f16 = p.out_f16 != 0;
+  out[lane] = out_bits_rt(o0 * inv, f16) | (out_bits_rt(o1 * inv, f16) << 16);
 }
 
 }  // namespace nvamd

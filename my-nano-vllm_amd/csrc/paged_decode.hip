@@ -14,7 +14,8 @@
 //     S^T[token][col] = K[token][:] . Q[col][:]      4 x v_mfma_f32_16x16x32_bf16 per column block
 //     O^T[dim][col]  += V^T[dim][token] . P^T[token][col]   8 x v_mfma_f32_16x16x16_f16
 // The FP8 cache bytes are converted exactly, K to bf16 and V to fp16, with
-// v_cvt_scalef32_pk_{bf16,f16}_fp8 (scale 1.0).  The softmax weights P are
+// v_cvt_scalef32_pk_{bf16,f16}_fp8 (scale 1.0).  fp16 queries (F16) take
+// v_mfma_f32_16x16x32_f16 for S with K converted to fp16.  The softmax weights P are
 // rounded to fp16 (11-bit significand; the lazy rescale keeps them below
 // 2^8), and the row sum adds those rounded weights, so numerator and
 // denominator use the same P.
@@ -70,10 +71,12 @@ __device__ __forceinline__ void load_chunk(ChunkRegs& cr, __amdgpu_buffer_rsrc_t
   for (int e = 0; e < 4; ++e) cr.v[e] = buf_load8(rv, v_off + (uint32_t)e * rs);
 }
 
-// 8 fp8 bytes (two dwords) -> bf16x8 (exact).
-__device__ __forceinline__ bf16x8 fp8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
-  return as_bf16x8(fp8x2_to_bf16x2<false>(lo), fp8x2_to_bf16x2<true>(lo),
-                   fp8x2_to_bf16x2<false>(hi), fp8x2_to_bf16x2<true>(hi));
+// 8 fp8 bytes (two dwords) -> 8 bf16 (or fp16 with F16) as four dwords (exact).
+template <bool F16>
+__device__ __forceinline__ u32x4 fp8x8_to(uint32_t lo, uint32_t hi) {
+  using QT = QkType<F16>;
+  return u32x4{QT::template k2<false>(lo), QT::template k2<true>(lo), QT::template k2<false>(hi),
+               QT::template k2<true>(hi)};
 }
 
 __device__ __forceinline__ f16x4 as_f16x4(uint32_t a, uint32_t b) {
@@ -107,24 +110,25 @@ __device__ __forceinline__ float col_max(float x) {
   return pair_max(b0, b1);
 }
 
-template <int NCB>
-__device__ __forceinline__ void attend_chunk(const ChunkRegs& cr, const bf16x8 (&qop)[NCB][4],
+template <int NCB, bool F16>
+__device__ __forceinline__ void attend_chunk(const ChunkRegs& cr, const typename QkType<F16>::V8 (&qop)[NCB][4],
                                              const int (&col_limit)[NCB], int tok0, bool need_mask,
                                              float scale_log2, int gam, float (&m)[NCB],
                                              float (&lsum)[NCB], f32x4 (&acc)[NCB][8]) {
   // ---- S^T = K . Q^T -------------------------------------------------------
-  bf16x8 kop[4];
+  using QT = QkType<F16>;
+  typename QT::V8 kop[4];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    kop[2 * h + 0] = fp8x8_to_bf16x8(cr.k[h].x, cr.k[h].y);
-    kop[2 * h + 1] = fp8x8_to_bf16x8(cr.k[h].z, cr.k[h].w);
+    kop[2 * h + 0] = QT::from_bits(fp8x8_to<F16>(cr.k[h].x, cr.k[h].y));
+    kop[2 * h + 1] = QT::from_bits(fp8x8_to<F16>(cr.k[h].z, cr.k[h].w));
   }
   f32x4 s[NCB];
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) {
     f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int c = 0; c < 4; ++c) a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[c], qop[cb][c], a, 0, 0, 0);
+    for (int c = 0; c < 4; ++c) a = QT::mfma16(kop[c], qop[cb][c], a);
     s[cb] = a;
   }
 
@@ -208,12 +212,14 @@ __device__ __forceinline__ SeqGeom seq_geom(const MqParams& p, int seq) {
   return sg;
 }
 
+template <bool F16>
 __device__ __forceinline__ void store_out_row8(uint16_t* __restrict__ dst, const float* o, float inv) {
+  using QT = QkType<F16>;
   u32x4 w;
-  w.x = out_round_bf16_bits(o[0] * inv) | (out_round_bf16_bits(o[1] * inv) << 16);
-  w.y = out_round_bf16_bits(o[2] * inv) | (out_round_bf16_bits(o[3] * inv) << 16);
-  w.z = out_round_bf16_bits(o[4] * inv) | (out_round_bf16_bits(o[5] * inv) << 16);
-  w.w = out_round_bf16_bits(o[6] * inv) | (out_round_bf16_bits(o[7] * inv) << 16);
+  w.x = QT::out_bits(o[0] * inv) | (QT::out_bits(o[1] * inv) << 16);
+  w.y = QT::out_bits(o[2] * inv) | (QT::out_bits(o[3] * inv) << 16);
+  w.z = QT::out_bits(o[4] * inv) | (QT::out_bits(o[5] * inv) << 16);
+  w.w = QT::out_bits(o[6] * inv) | (QT::out_bits(o[7] * inv) << 16);
   *reinterpret_cast<u32x4*>(dst) = w;
 }
 
@@ -249,7 +255,8 @@ constexpr int kRingBytes = kStages * 16384;
 // Makes the compiler wait here for the loads that produced x (an empty asm
 // that reads it), so no load of x is still counted as pending inside the
 // main loop, where the compiler would otherwise wait for every load in flight.
-__device__ __forceinline__ void consume(const bf16x8& x) { asm volatile("" ::"v"(x)); }
+template <typename T>
+__device__ __forceinline__ void consume(const T& x) { asm volatile("" ::"v"(x)); }
 __device__ __forceinline__ void consume_i32(int x) { asm volatile("" ::"v"(x)); }
 
 __device__ __forceinline__ u32x4 lds_read16(const uint8_t* a) { return *reinterpret_cast<const u32x4*>(a); }
@@ -259,9 +266,10 @@ __device__ __forceinline__ u32x2 lds_read8(const uint8_t* a) { return *reinterpr
 
 // Work item (partition `part`, kv head group `hg`: heads hg*HG .. hg*HG+HG-1,
 // sequence `seq`) of the split-KV kernel.
-template <int NCB, int HG>
+template <int NCB, int HG, bool F16>
 __device__ __forceinline__ void mq_attn(const MqParams& p, const int part, const int hg, const int seq) {
   using S = Stage<HG>;
+  using QT = QkType<F16>;
   __shared__ __attribute__((aligned(16))) uint8_t smem[kRingBytes];
   const uint32_t lds_smem = wave_uniform((int)lds_addr(smem));
 
@@ -295,7 +303,7 @@ __device__ __forceinline__ void mq_attn(const MqParams& p, const int part, const
   const int n_parts = (sg.Lk + p.part_tokens - 1) / p.part_tokens;
 
   // ---- query operands ------------------------------------------------------
-  bf16x8 qop[NCB][4];
+  typename QT::V8 qop[NCB][4];
   int col_limit[NCB];
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) {
@@ -312,8 +320,8 @@ __device__ __forceinline__ void mq_attn(const MqParams& p, const int part, const
         a = *reinterpret_cast<const u32x4*>(qp);
         b = *reinterpret_cast<const u32x4*>(qp + 8);
       }
-      qop[cb][2 * h + 0] = as_bf16x8(a);
-      qop[cb][2 * h + 1] = as_bf16x8(b);
+      qop[cb][2 * h + 0] = QT::from_bits(a);
+      qop[cb][2 * h + 1] = QT::from_bits(b);
     }
   }
 
@@ -445,8 +453,8 @@ __device__ __forceinline__ void mq_attn(const MqParams& p, const int part, const
     cr.k[1] = lds_read16(sl + k_rd[1]);
 #pragma unroll
     for (int e = 0; e < 4; ++e) cr.v[e] = lds_read8(sl + v_rd[e]);
-    attend_chunk<NCB>(cr, qop, col_limit, tok0, tok0 + kChunk > mask_from, p.scale_log2, gam, m, lsum,
-                      acc);
+    attend_chunk<NCB, F16>(cr, qop, col_limit, tok0, tok0 + kChunk > mask_from, p.scale_log2, gam, m, lsum,
+                           acc);
     tok0 += S::kTS;
   }
 
@@ -518,7 +526,7 @@ __device__ __forceinline__ void mq_attn(const MqParams& p, const int part, const
         const int64_t rh = row * p.Hq + (hg * HG + oh) * G + gh;
         if (n_parts == 1) {
           const float inv = (L > 0.f) ? 1.0f / L : 0.f;
-          store_out_row8(p.out + rh * kHeadDim + d0, o, inv);
+          store_out_row8<F16>(p.out + rh * kHeadDim + d0, o, inv);
         } else {
           const int64_t pi = rh * p.max_parts + part;
           float* pa = p.part_acc + pi * kHeadDim + d0;
@@ -535,22 +543,22 @@ __device__ __forceinline__ void mq_attn(const MqParams& p, const int part, const
   }
 }
 
-template <int NCB, int HG>
+template <int NCB, int HG, bool F16>
 __global__ __launch_bounds__(256) void paged_mq_attn_kernel(MqParams p) {
-  mq_attn<NCB, HG>(p, blockIdx.x, blockIdx.y, blockIdx.z);
+  mq_attn<NCB, HG, F16>(p, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
 // Short-query pass of a prefill call, with one more z-slice whose first
 // workgroup writes the prefill kernel's work list (the prefill kernel is the
 // next launch on the stream).
-template <int NCB, int HG>
+template <int NCB, int HG, bool F16>
 __global__ __launch_bounds__(256) void prefill_short_kernel(MqParams p, PrefillParams pp, PrefillItem* items) {
   if ((int)blockIdx.z == p.num_seqs) {
     __shared__ int sched_lds[kScheduleLdsInts];
     if (blockIdx.x == 0 && blockIdx.y == 0) prefill_schedule(pp, items, sched_lds);
     return;
   }
-  mq_attn<NCB, HG>(p, blockIdx.x, blockIdx.y, blockIdx.z);
+  mq_attn<NCB, HG, F16>(p, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
 // Decode mode: one wave per (sequence, head).
@@ -645,9 +653,10 @@ struct SkStage {
 // A prefill call with long sequences launches one workgroup more (index
 // sk_wgs, resident beside the sk_wgs stream-K workgroups) that writes the
 // prefill kernel's work list (items != nullptr).
-template <int NCB, int HG, bool QL>
+template <int NCB, int HG, bool QL, bool F16>
 __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p, PrefillParams pp, PrefillItem* items) {
   using S = SkStage<HG, QL>;
+  using QT = QkType<F16>;
   static_assert(HG == 4 || HG == 8, "4 or 8 kv heads per workgroup");
   static_assert(!QL || NCB == 1, "queries through LDS for G <= 8 only");
   constexpr int kRingBytes = S::kRing;
@@ -835,7 +844,7 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p, PrefillP
   int cL = L0;
   bool first_seg = true;
   int seg_o0 = o0;
-  bf16x8 qop[NCB][4];
+  typename QT::V8 qop[NCB][4];
   int col_limit[NCB];
   int64_t col_row[NCB];  // output / query element offset of the lane's column, -1 if unused
   int mask_from = 0;     // first key position that some column of the pair cannot see
@@ -878,8 +887,8 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p, PrefillP
             a = *reinterpret_cast<const u32x4*>(qp);
             b = *reinterpret_cast<const u32x4*>(qp + 8);
           }
-          qop[cb][2 * h + 0] = as_bf16x8(a);
-          qop[cb][2 * h + 1] = as_bf16x8(b);
+          qop[cb][2 * h + 0] = QT::from_bits(a);
+          qop[cb][2 * h + 1] = QT::from_bits(b);
         }
       }
       m[cb] = -INFINITY;
@@ -906,7 +915,7 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p, PrefillP
       for (int j = 0; j < 2; ++j) {
         u32x4 a = {0u, 0u, 0u, 0u};
         if (valid) a = lds_read16(qa + (wave * G + col) * (kHeadDim * 2) + (16 * gam + 64 * h + 8 * j) * 2);
-        qop[0][2 * h + j] = as_bf16x8(a);
+        qop[0][2 * h + j] = QT::from_bits(a);
       }
   };
   // Writes the output of a pair finished here, or the partial of a cut pair.
@@ -925,7 +934,7 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p, PrefillP
           float o[8];
 #pragma unroll
           for (int i = 0; i < 8; ++i) o[i] = acc[cb][i][k];
-          store_out_row8(op + 8 * k, o, inv);
+          store_out_row8<F16>(op + 8 * k, o, inv);
         }
       } else {
         const int slot = first_seg ? 0 : 1;
@@ -968,7 +977,8 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p, PrefillP
 #pragma unroll
     for (int e = 0; e < 4; ++e) cr.v[e] = lds_read8(sl + v_rd[e]);
     const int tok0 = co * kSkStageTokens;
-    attend_chunk<NCB>(cr, qop, col_limit, tok0, tok0 + kSkStageTokens > mask_from, p.scale_log2, gam, m, lsum, acc);
+    attend_chunk<NCB, F16>(cr, qop, col_limit, tok0, tok0 + kSkStageTokens > mask_from, p.scale_log2, gam, m, lsum,
+                           acc);
     if (++co == cn || s == n_w - 1) {
       end_segment(seg_o0 == 0 && co == cn);
       if (s < n_w - 1) {
@@ -1001,7 +1011,10 @@ int sk_occupancy() {
   static std::atomic<int> cached{0};  // the kernel's occupancy does not change
   int n = cached.load(std::memory_order_relaxed);
   if (n > 0) return n;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_sk_kernel<NCB, HG, QL>, 64 * HG, 0) != hipSuccess ||
+  // the fp16 instances use the same registers and LDS (the workspace size,
+  // which depends on the grid, does not depend on the query type)
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_sk_kernel<NCB, HG, QL, false>, 64 * HG, 0) !=
+          hipSuccess ||
       n <= 0)
     return 1;  // no device: not cached
   cached.store(n, std::memory_order_relaxed);
@@ -1048,12 +1061,21 @@ hipError_t launch_decode_sk(const MqParams& p, int ncb, bool merge, const Prefil
     it = static_cast<PrefillItem*>(items);
   }
   const dim3 grid((unsigned)p.sk_wgs + (it != nullptr ? 1u : 0u)), block((unsigned)(64 * hg));
-  switch (sk_variant(ncb, hg, p.G, varlen)) {
-    case 0: hipLaunchKernelGGL((decode_sk_kernel<1, 4, false>), grid, block, 0, stream, p, ppv, it); break;
-    case 1: hipLaunchKernelGGL((decode_sk_kernel<2, 4, false>), grid, block, 0, stream, p, ppv, it); break;
-    case 2: hipLaunchKernelGGL((decode_sk_kernel<1, 8, true>), grid, block, 0, stream, p, ppv, it); break;
-    case 3: hipLaunchKernelGGL((decode_sk_kernel<1, 8, false>), grid, block, 0, stream, p, ppv, it); break;
-    default: hipLaunchKernelGGL((decode_sk_kernel<2, 8, false>), grid, block, 0, stream, p, ppv, it); break;
+  switch (2 * sk_variant(ncb, hg, p.G, varlen) + (p.out_f16 ? 1 : 0)) {
+#define NVAMD_SK_CASE(c, NCB, HG, QL, F16)                                                                   \
+  case c: hipLaunchKernelGGL((decode_sk_kernel<NCB, HG, QL, F16>), grid, block, 0, stream, p, ppv, it); break;
+    NVAMD_SK_CASE(0, 1, 4, false, false)
+    NVAMD_SK_CASE(1, 1, 4, false, true)
+    NVAMD_SK_CASE(2, 2, 4, false, false)
+    NVAMD_SK_CASE(3, 2, 4, false, true)
+    NVAMD_SK_CASE(4, 1, 8, true, false)
+    NVAMD_SK_CASE(5, 1, 8, true, true)
+    NVAMD_SK_CASE(6, 1, 8, false, false)
+    NVAMD_SK_CASE(7, 1, 8, false, true)
+    NVAMD_SK_CASE(8, 2, 8, false, false)
+    NVAMD_SK_CASE(9, 2, 8, false, true)
+#undef NVAMD_SK_CASE
+    default: return hipErrorInvalidValue;
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -1068,11 +1090,19 @@ hipError_t launch_prefill_short(const MqParams& p, int ncb, const PrefillParams&
   const int hg = (p.Hkv % 2 == 0) ? 2 : 1;  // kv heads per workgroup
   const dim3 grid((unsigned)p.max_parts, (unsigned)(p.Hkv / hg), (unsigned)p.num_seqs + 1u);
   PrefillItem* it = static_cast<PrefillItem*>(items);
-  switch (2 * (ncb - 1) + (hg - 1)) {
-    case 0: hipLaunchKernelGGL((prefill_short_kernel<1, 1>), grid, dim3(256), 0, stream, p, pp, it); break;
-    case 1: hipLaunchKernelGGL((prefill_short_kernel<1, 2>), grid, dim3(256), 0, stream, p, pp, it); break;
-    case 2: hipLaunchKernelGGL((prefill_short_kernel<2, 1>), grid, dim3(256), 0, stream, p, pp, it); break;
-    case 3: hipLaunchKernelGGL((prefill_short_kernel<2, 2>), grid, dim3(256), 0, stream, p, pp, it); break;
+  if (ncb != 1 && ncb != 2) return hipErrorInvalidValue;
+  switch (4 * (ncb - 1) + 2 * (hg - 1) + (p.out_f16 ? 1 : 0)) {
+#define NVAMD_PS_CASE(c, NCB, HG, F16)                                                                        \
+  case c: hipLaunchKernelGGL((prefill_short_kernel<NCB, HG, F16>), grid, dim3(256), 0, stream, p, pp, it); break;
+    NVAMD_PS_CASE(0, 1, 1, false)
+    NVAMD_PS_CASE(1, 1, 1, true)
+    NVAMD_PS_CASE(2, 1, 2, false)
+    NVAMD_PS_CASE(3, 1, 2, true)
+    NVAMD_PS_CASE(4, 2, 1, false)
+    NVAMD_PS_CASE(5, 2, 1, true)
+    NVAMD_PS_CASE(6, 2, 2, false)
+    NVAMD_PS_CASE(7, 2, 2, true)
+#undef NVAMD_PS_CASE
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -1082,12 +1112,19 @@ hipError_t launch_paged_mq(const MqParams& p, int ncb, hipStream_t stream) {
   if (p.num_seqs == 0) return hipSuccess;
   const int hg = (p.Hkv % 2 == 0) ? 2 : 1;  // kv heads per workgroup
   const dim3 grid((unsigned)p.max_parts, (unsigned)(p.Hkv / hg), (unsigned)p.num_seqs);
-  const int variant = 2 * (ncb - 1) + (hg - 1);
-  switch (variant) {
-    case 0: hipLaunchKernelGGL((paged_mq_attn_kernel<1, 1>), grid, dim3(256), 0, stream, p); break;
-    case 1: hipLaunchKernelGGL((paged_mq_attn_kernel<1, 2>), grid, dim3(256), 0, stream, p); break;
-    case 2: hipLaunchKernelGGL((paged_mq_attn_kernel<2, 1>), grid, dim3(256), 0, stream, p); break;
-    case 3: hipLaunchKernelGGL((paged_mq_attn_kernel<2, 2>), grid, dim3(256), 0, stream, p); break;
+  if (ncb != 1 && ncb != 2) return hipErrorInvalidValue;
+  switch (4 * (ncb - 1) + 2 * (hg - 1) + (p.out_f16 ? 1 : 0)) {
+#define NVAMD_MQ_CASE(c, NCB, HG, F16)                                                                   \
+  case c: hipLaunchKernelGGL((paged_mq_attn_kernel<NCB, HG, F16>), grid, dim3(256), 0, stream, p); break;
+    NVAMD_MQ_CASE(0, 1, 1, false)
+    NVAMD_MQ_CASE(1, 1, 1, true)
+    NVAMD_MQ_CASE(2, 1, 2, false)
+    NVAMD_MQ_CASE(3, 1, 2, true)
+    NVAMD_MQ_CASE(4, 2, 1, false)
+    NVAMD_MQ_CASE(5, 2, 1, true)
+    NVAMD_MQ_CASE(6, 2, 2, false)
+    NVAMD_MQ_CASE(7, 2, 2, true)
+#undef NVAMD_MQ_CASE
     default: return hipErrorInvalidValue;
   }
   hipError_t e = hipGetLastError();

@@ -21,14 +21,14 @@
 // stage K tiles, waves 4..7 V tiles: each thread loads its share of an FP8
 // tile into registers a step ahead (bounded raw buffer loads: rows past the
 // sequence read as zero, so every iteration issues the same loads and the
-// compiler's wait counts stay exact), converts it exactly -- K to bf16, V to
-// fp16 -- and stages it in one of two LDS buffers, K as [token][dim], V
+// compiler's wait counts stay exact), converts it exactly -- K to bf16 (to
+// fp16 for fp16 queries), V to fp16 -- and stages it in one of two LDS buffers, K as [token][dim], V
 // transposed as [dim][token].  One barrier per tile.  Each K load
 // instruction fetches 8 rows (8 lanes per row), each V load instruction 4
 // whole rows.
 //
 // Per tile a wave computes (fp32 accumulate)
-//     S^T[kv][q] = K[kv][:] . Q[q][:]          v_mfma_f32_32x32x16_bf16, 2 row blocks x 8 k-steps
+//     S^T[kv][q] = K[kv][:] . Q[q][:]          v_mfma_f32_32x32x16_bf16 (_f16), 2 row blocks x 8 k-steps
 //     O^T[d][q] += V^T[d][kv] . P^T[kv][q]     v_mfma_f32_32x32x16_f16,  4 dim blocks x 4 k-steps
 // The softmax weights P are rounded to fp16 (11-bit significand; the lazy
 // rescale keeps them <= 2^8), V is exact in fp16.  Lane l (h = l / 32) holds
@@ -118,10 +118,11 @@ __device__ __forceinline__ void pin(T& v) { asm volatile("" : "+v"(v)); }
 // ---------------------------------------------------------------------------
 // Main kernel
 // ---------------------------------------------------------------------------
-template <bool PAGED, bool SMALL_BLOCKS>
+template <bool PAGED, bool SMALL_BLOCKS, bool F16>
 __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(PrefillParams p,
                                                                               const PrefillItem* __restrict__ items,
                                                                               MqParams mq, int n_main) {
+  using QT = QkType<F16>;
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kBufElems];
 
   // Workgroups past the items merge the split-KV partitions of the
@@ -226,12 +227,12 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
       dma_load16_keep(qr, (uint32_t)r * row_bytes + 16 * (slot ^ (r & 15)), lds_addr(qs + 4 * j * kQRowBytes));
     }
   }
-  bf16x8 qop[8];
+  typename QT::V8 qop[8];
   auto q_to_operands = [&] {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the Q loads (and every later load) have landed
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks)
-      qop[ks] = as_bf16x8(*reinterpret_cast<const u32x4*>(qs + col * kQRowBytes + 16 * ((2 * ks + h) ^ (col & 15))));
+      qop[ks] = QT::from_bits(*reinterpret_cast<const u32x4*>(qs + col * kQRowBytes + 16 * ((2 * ks + h) ^ (col & 15))));
   };
 
   f32x16 acc[4];
@@ -334,15 +335,15 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
     }
   };
 
-  // Converts a K tile share to bf16 and writes it to K buffer kb, in four
+  // Converts a K tile share to bf16 (fp16 with F16) and writes it to K buffer kb, in four
   // quarters (one 16-byte store each) that can be spread over a stretch of
   // MFMAs.
   const int k_lds[2] = {k_row * kKPitch + k_byte + k_first, k_row * kKPitch + k_byte + (k_first ^ 8)};
   auto stage_k_q = [&](const TileRegs& kr, uint16_t* kb, int i) {
     const u32x2 w = kr.r[i];
     u32x4 o;
-    o.x = fp8x2_to_bf16x2<false>(w.x); o.y = fp8x2_to_bf16x2<true>(w.x);
-    o.z = fp8x2_to_bf16x2<false>(w.y); o.w = fp8x2_to_bf16x2<true>(w.y);
+    o.x = QT::template k2<false>(w.x); o.y = QT::template k2<true>(w.x);
+    o.z = QT::template k2<false>(w.y); o.w = QT::template k2<true>(w.y);
     *reinterpret_cast<u32x4*>(kb + k_lds[i & 1] + (i >> 1) * 32 * kKPitch) = o;
   };
   auto stage_k = [&](const TileRegs& kr, uint16_t* kb) {
@@ -484,7 +485,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
       const u32x4 cur = pre[i % kLead];
       if (i + kLead < 16) pre[i % kLead] = *reinterpret_cast<const u32x4*>(kaddr(i + kLead));
       else vpre[i + kLead - 16] = *reinterpret_cast<const u32x4*>(vaddr(vb, i + kLead - 16));
-      s_next[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(cur), qop[i >> 1], s_next[i & 1], 0, 0, 0);
+      s_next[i & 1] = QT::mfma32(QT::from_bits(cur), qop[i >> 1], s_next[i & 1]);
       if (i < 12) exp_pair(s_cur, 4 + i, pw, ps_pend);
     }
     // the first exponentials run while the first K operands are in flight
@@ -628,9 +629,9 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
       const uint16_t* kr = kbuf0 + col * kKPitch + 8 * h;
 #pragma unroll
       for (int i = 0; i < 16; ++i)
-        sa[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            as_bf16x8(*reinterpret_cast<const u32x4*>(kr + (i & 1) * 32 * kKPitch + 16 * (i >> 1))), qop[i >> 1],
-            sa[i & 1], 0, 0, 0);
+        sa[i & 1] = QT::mfma32(
+            QT::from_bits(*reinterpret_cast<const u32x4*>(kr + (i & 1) * 32 * kKPitch + 16 * (i >> 1))), qop[i >> 1],
+            sa[i & 1]);
       mask_tile(t0, t1, sa);
       float alpha;
       if (update_max(sa, alpha)) rescale_acc(alpha);
@@ -808,8 +809,8 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
       for (int b4 = 0; b4 < 4; ++b4) {
         const int d = 32 * db + 8 * b4 + 4 * h;
         u32x2 w;
-        w.x = out_round_bf16_bits(acc[db][4 * b4 + 0] * inv) | (out_round_bf16_bits(acc[db][4 * b4 + 1] * inv) << 16);
-        w.y = out_round_bf16_bits(acc[db][4 * b4 + 2] * inv) | (out_round_bf16_bits(acc[db][4 * b4 + 3] * inv) << 16);
+        w.x = QT::out_bits(acc[db][4 * b4 + 0] * inv) | (QT::out_bits(acc[db][4 * b4 + 1] * inv) << 16);
+        w.y = QT::out_bits(acc[db][4 * b4 + 2] * inv) | (QT::out_bits(acc[db][4 * b4 + 3] * inv) << 16);
         *reinterpret_cast<u32x2*>(ob + col * kOPitch + d) = w;
       }
     }
@@ -839,12 +840,22 @@ hipError_t launch_varlen_prefill(const PrefillParams& p, const void* schedule, c
   if (n_blocks + n_merge > 0x7fffffff || schedule == nullptr) return hipErrorInvalidValue;
   const dim3 grid((unsigned)(n_blocks + n_merge)), block(64 * kPrefillWaves);
   const PrefillItem* items = static_cast<const PrefillItem*>(schedule);
-  if (p.block_tables == nullptr)
-    hipLaunchKernelGGL((varlen_prefill_kernel<false, false>), grid, block, 0, stream, p, items, mq, (int)n_blocks);
-  else if (p.block_size % kBN == 0)
-    hipLaunchKernelGGL((varlen_prefill_kernel<true, false>), grid, block, 0, stream, p, items, mq, (int)n_blocks);
-  else
-    hipLaunchKernelGGL((varlen_prefill_kernel<true, true>), grid, block, 0, stream, p, items, mq, (int)n_blocks);
+  const int layout = p.block_tables == nullptr ? 0 : (p.block_size % kBN == 0 ? 1 : 2);
+  switch (2 * layout + (p.out_f16 ? 1 : 0)) {
+#define NVAMD_VP_CASE(c, PAGED, SMALL, F16)                                                                   \
+  case c:                                                                                                     \
+    hipLaunchKernelGGL((varlen_prefill_kernel<PAGED, SMALL, F16>), grid, block, 0, stream, p, items, mq,      \
+                       (int)n_blocks);                                                                        \
+    break;
+    NVAMD_VP_CASE(0, false, false, false)
+    NVAMD_VP_CASE(1, false, false, true)
+    NVAMD_VP_CASE(2, true, false, false)
+    NVAMD_VP_CASE(3, true, false, true)
+    NVAMD_VP_CASE(4, true, true, false)
+    NVAMD_VP_CASE(5, true, true, true)
+#undef NVAMD_VP_CASE
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

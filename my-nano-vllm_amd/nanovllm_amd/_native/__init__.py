@@ -16,7 +16,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime first)
 
 LIB_NAME = "libnvamd_fp8attn.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _c_void_p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -28,17 +28,17 @@ SIGNATURES = {
     "nvamd_abi_version": (_i32, []),
     "nvamd_last_error": (ctypes.c_char_p, []),
     "nvamd_store_kvcache": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p,
-                                   _c_void_p, _i64, _i32, _i32, _i64, _c_void_p]),
+                                   _c_void_p, _i64, _i32, _i32, _i64, _i32, _c_void_p]),
     "nvamd_qk_norm_rope_store": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _f32, _c_void_p, _i64,
                                         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i32,
                                         _i32, _i64, _c_void_p]),
     "nvamd_decode_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "nvamd_fp8_decode_attention": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                           _c_void_p, _i32, _i32, _i32, _i32, _i64, _i32, _i32,
-                                          _f32, _i32, _c_void_p, _i64, _c_void_p]),
+                                          _f32, _i32, _c_void_p, _i64, _i32, _c_void_p]),
     "nvamd_fp8_decode_attention_noalloc": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                                   _c_void_p, _i32, _i32, _i32, _i32, _i64, _i32, _i32,
-                                                  _f32, _c_void_p]),
+                                                  _f32, _i32, _c_void_p]),
     "nvamd_build_attention_metadata": (_i32, [_c_void_p, _i64, _i32, _i32, _i32, _i64, _i64, _i32, _i32,
                                               _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                               _c_void_p]),
@@ -54,7 +54,7 @@ SIGNATURES = {
     "nvamd_fp8_prefill_attention": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                            _c_void_p, _c_void_p, _i64, _i32, _i32, _i32, _i32,
                                            _i64, _i32, _i32, _i32, _i32, _f32, _i32, _c_void_p,
-                                           _i64, _c_void_p]),
+                                           _i64, _i32, _c_void_p]),
 }
 
 _lib = None

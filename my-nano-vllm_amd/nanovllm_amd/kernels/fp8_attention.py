@@ -18,6 +18,8 @@ import torch
 from .. import _native
 
 _FP8 = torch.float8_e4m3fn
+# element type codes of the C ABI (NVAMD_DTYPE_BF16 / NVAMD_DTYPE_F16)
+_QO_DTYPES = {torch.bfloat16: 0, torch.float16: 1}
 
 
 def _require(cond, msg):
@@ -30,6 +32,11 @@ def _dev_tensor(t, name, dtype=None):
     _require(t.is_cuda, f"{name} must be on a ROCm GPU (got {t.device})")
     if dtype is not None:
         _require(t.dtype == dtype, f"{name} must be {dtype} (got {t.dtype})")
+
+
+def _qo_dtype(q):
+    _require(q.dtype in _QO_DTYPES, f"q must be bfloat16 or float16 (got {q.dtype})")
+    return _QO_DTYPES[q.dtype]
 
 
 def _int32(t, name):
@@ -55,7 +62,7 @@ def fp8_decode_attention(
 ) -> torch.Tensor:
     """
     Args:
-        q: [batch_size, num_heads, head_dim] bf16
+        q: [batch_size, num_heads, head_dim] bf16 or fp16
         k_cache: [num_blocks, block_size, num_kv_heads, head_dim] (FP8 E4M3FN)
         v_cache: same as k_cache
         block_tables: [batch_size, max_num_blocks] int32
@@ -63,11 +70,12 @@ def fp8_decode_attention(
         softmax_scale: attention scaling factor (1/sqrt(head_dim))
 
     Returns:
-        [batch_size, num_heads, head_dim] bf16 attention output
+        [batch_size, num_heads, head_dim] attention output of q's dtype
         (rows with context_lens == 0 are zero).
     """
     lib = _native.load()
-    _dev_tensor(q, "q", torch.bfloat16)
+    _dev_tensor(q, "q")
+    qo_dtype = _qo_dtype(q)
     _dev_tensor(k_cache, "k_cache", _FP8)
     _dev_tensor(v_cache, "v_cache", _FP8)
     _require(q.dim() == 3, "q must be [batch, num_heads, head_dim]")
@@ -95,7 +103,7 @@ def fp8_decode_attention(
         out.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
         block_tables.data_ptr(), context_lens.data_ptr(),
         batch_size, num_heads, num_kv_heads, head_dim, num_blocks, block_size, max_num_blocks,
-        float(softmax_scale), 0, ws.data_ptr() if ws is not None else None, ws_bytes,
+        float(softmax_scale), 0, ws.data_ptr() if ws is not None else None, ws_bytes, qo_dtype,
         _stream_ptr(q.device))
     _native.check(status, "fp8_decode_attention")
     return out
@@ -109,7 +117,7 @@ def fp8_prefill_attention(
     """Varlen causal (chunked) prefill with FP8 K/V.
 
     Args:
-        q: [num_tokens, num_heads, head_dim] bf16
+        q: [num_tokens, num_heads, head_dim] bf16 or fp16 (the output's dtype)
         k, v: paged caches [num_blocks, block_size, num_kv_heads, head_dim]
               when block_tables is given, else contiguous [num_kv_tokens,
               num_kv_heads, head_dim]; FP8 E4M3FN
@@ -122,7 +130,8 @@ def fp8_prefill_attention(
     Query row i of sequence s attends to keys j <= i + (Lk - Lq).
     """
     lib = _native.load()
-    _dev_tensor(q, "q", torch.bfloat16)
+    _dev_tensor(q, "q")
+    qo_dtype = _qo_dtype(q)
     _dev_tensor(k, "k", _FP8)
     _dev_tensor(v, "v", _FP8)
     _require(q.dim() == 3, "q must be [num_tokens, num_heads, head_dim]")
@@ -164,6 +173,6 @@ def fp8_prefill_attention(
         cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(),
         num_tokens, num_seqs, num_heads, num_kv_heads, head_dim, num_kv_rows, block_size,
         max_num_blocks, max_seqlen_q, int(max_seqlen_k), float(softmax_scale), 0,
-        ws.data_ptr() if ws is not None else None, ws_bytes, _stream_ptr(q.device))
+        ws.data_ptr() if ws is not None else None, ws_bytes, qo_dtype, _stream_ptr(q.device))
     _native.check(status, "fp8_prefill_attention")
     return out

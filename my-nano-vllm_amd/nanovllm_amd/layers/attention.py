@@ -24,8 +24,8 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
                     (slot_mapping, "slot_mapping")):
         if not t.is_cuda:
             raise ValueError(f"{name} must be on a ROCm GPU (got {t.device})")
-    if key.dtype != torch.bfloat16 or value.dtype != torch.bfloat16:
-        raise ValueError("key/value must be bf16")
+    if key.dtype not in (torch.bfloat16, torch.float16) or value.dtype != key.dtype:
+        raise ValueError(f"key/value must both be bf16 or both fp16 (got {key.dtype}, {value.dtype})")
     if k_cache.dtype != torch.float8_e4m3fn or v_cache.dtype != torch.float8_e4m3fn:
         raise ValueError("k_cache/v_cache must be float8_e4m3fn")
     if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
@@ -39,5 +39,5 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
     status = lib.nvamd_store_kvcache(
         key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0),
         k_cache.data_ptr(), v_cache.data_ptr(), slot_mapping.data_ptr(), N, num_heads, head_dim,
-        num_slots, torch.cuda.current_stream(key.device).cuda_stream)
+        num_slots, 1 if key.dtype == torch.float16 else 0, torch.cuda.current_stream(key.device).cuda_stream)
     _native.check(status, "store_kvcache")

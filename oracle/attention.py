@@ -7,8 +7,9 @@ Follows the reference kernels' semantics, not their tiling:
   ``context_lens[b]`` cached tokens, gathered through ``block_tables[b]``
   (token t lives at slot ``bt[b, t // bs] * bs + t % bs``, :127-142).
   Scores are ``(q . k) * softmax_scale`` (:153), softmax over the context,
-  ``out = acc / max(s, 1e-10)`` cast to fp16 (:169) and stored into a bf16
-  tensor (``empty_like(q)``, :193) -- i.e. fp32 -> fp16 -> bf16.
+  ``out = acc / max(s, 1e-10)`` cast to fp16 (:169) and stored into
+  ``empty_like(q)`` (:193) -- i.e. fp32 -> fp16 -> bf16 for bf16 queries,
+  fp32 -> fp16 for fp16 queries.
   ``context_lens[b] == 0`` yields NaN in the reference (exp(-inf - -inf));
   the oracle returns NaN there too and callers treat such rows as
   don't-care.
@@ -19,7 +20,7 @@ Follows the reference kernels' semantics, not their tiling:
   paged cache through ``block_tables[s]`` (:280-308) or, when
   ``block_tables is None``, from the contiguous ``k[cu_k[s] + j]`` (:254-278).
   Rows whose softmax denominator is 0 output 0 (:311); output is
-  fp32 -> fp16 -> bf16 (:311, :337).
+  fp32 -> fp16 -> q's dtype (:311, :337).
 * The FP8 cache is dequantised exactly (``.to(tl.float32)``; scale 1).
 
 ``compute_dtype`` selects float32 (the reference's accumulation type) or
@@ -37,9 +38,10 @@ def _as_codes(t):
     return t
 
 
-def round_output(x):
-    """fp32 attention output -> bf16 through fp16, as the reference stores it."""
-    return x.to(torch.float32).to(torch.float16).to(torch.bfloat16)
+def round_output(x, dtype=torch.bfloat16):
+    """fp32 attention output -> fp16 -> the output dtype (q's: bf16 or fp16),
+    as the reference stores it."""
+    return x.to(torch.float32).to(torch.float16).to(dtype)
 
 
 def _gather_paged(cache_codes, table_row, n_tokens, kv_head):
@@ -73,9 +75,10 @@ def decode_attention(q, k_cache, v_cache, block_tables, context_lens, softmax_sc
                      compute_dtype=torch.float32, return_fp32=False):
     """Reference-semantics paged decode on the CPU.
 
-    q: bf16 [B, Hq, D]; k_cache/v_cache: uint8 or float8_e4m3fn
+    q: bf16 or fp16 [B, Hq, D]; k_cache/v_cache: uint8 or float8_e4m3fn
     [P, bs, Hkv, D]; block_tables: int [B, max_nb]; context_lens: int [B].
-    Returns bf16 [B, Hq, D] (or the unrounded result if ``return_fp32``).
+    Returns [B, Hq, D] of q's dtype (or the unrounded result if
+    ``return_fp32``).
     """
     kc, vc = _as_codes(k_cache), _as_codes(v_cache)
     B, Hq, D = q.shape
@@ -94,14 +97,14 @@ def decode_attention(q, k_cache, v_cache, block_tables, context_lens, softmax_sc
             limits = torch.full((G,), ctx, dtype=torch.int64)
             o, _ = _attend(qg, k, v, softmax_scale, limits, compute_dtype)
             out[b, g * G:(g + 1) * G] = o
-    return out if return_fp32 else round_output(out)
+    return out if return_fp32 else round_output(out, q.dtype)
 
 
 def prefill_attention(q, k, v, block_tables, cu_seqlens_q, cu_seqlens_k, softmax_scale,
                       compute_dtype=torch.float32, return_fp32=False):
     """Reference-semantics varlen causal prefill on the CPU.
 
-    q: bf16 [Nq, Hq, D].  Paged: k/v are caches [P, bs, Hkv, D] and
+    q: bf16 or fp16 [Nq, Hq, D] (the output's dtype).  Paged: k/v are caches [P, bs, Hkv, D] and
     block_tables int [S, max_nb].  Contiguous (block_tables is None): k/v are
     [Nk, Hkv, D] FP8 codes indexed by cu_seqlens_k.
     """
@@ -132,5 +135,5 @@ def prefill_attention(q, k, v, block_tables, cu_seqlens_q, cu_seqlens_k, softmax
             o, l = _attend(qg, kk, vv, softmax_scale, limits.repeat(G), compute_dtype)
             o = torch.where((l > 0).unsqueeze(1), o, torch.zeros_like(o))
             out[q0:q1, g * G:(g + 1) * G] = o.reshape(G, Lq, D).permute(1, 0, 2)
-    return out if return_fp32 else round_output(out)
+    return out if return_fp32 else round_output(out, q.dtype)
 

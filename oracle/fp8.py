@@ -124,12 +124,22 @@ def dequant_codes_tensor(codes):
     return table[codes.long()]
 
 
+def quantize_f16_tensor(t):
+    """torch fp16 tensor (CPU) -> torch uint8 tensor of E4M3FN codes: the
+    value widened to float32 (exact), then rounded as e4m3_encode does."""
+    import torch
+    vals = t.contiguous().to(torch.float32).numpy()
+    return torch.from_numpy(e4m3_encode(vals).reshape(tuple(t.shape)))
+
+
 def store_kvcache(key, value, k_cache, v_cache, slot_mapping):
     """CPU restatement of store_kvcache (nanovllm/layers/attention.py:11-40).
 
-    key/value: torch bf16 [N, Hkv, D] (any row stride); k_cache/v_cache:
-    torch uint8 [P, bs, Hkv, D] written in place; slot_mapping: int [N],
-    rows with slot == -1 are skipped (attention.py:24).
+    key/value: torch bf16 or fp16 [N, Hkv, D] (any row stride); the
+    reference's tl.store converts them to the cache's float8e4nv
+    (attention.py:30-31), rounding to nearest even with saturation.
+    k_cache/v_cache: torch uint8 [P, bs, Hkv, D] written in place;
+    slot_mapping: int [N], rows with slot == -1 are skipped (attention.py:24).
     """
     import torch
     N = key.shape[0]
@@ -138,8 +148,9 @@ def store_kvcache(key, value, k_cache, v_cache, slot_mapping):
     keep = slots != -1
     if N == 0 or not bool(keep.any()):
         return
-    kq = quantize_bf16_tensor(key.reshape(N, D)[keep])
-    vq = quantize_bf16_tensor(value.reshape(N, D)[keep])
+    quant = quantize_f16_tensor if key.dtype == torch.float16 else quantize_bf16_tensor
+    kq = quant(key.reshape(N, D)[keep])
+    vq = quant(value.reshape(N, D)[keep])
     kf = k_cache.view(-1, D)
     vf = v_cache.view(-1, D)
     kf[slots[keep]] = kq

@@ -21,14 +21,14 @@ def cpu_store(k, v, kc, vc, slots):
     ofp8.store_kvcache(k, v, kc.view(torch.uint8), vc.view(torch.uint8), slots)
 
 
-def build_pair(wl, include_new=True, gen_device="cpu"):
+def build_pair(wl, include_new=True, gen_device="cpu", dtype=torch.bfloat16):
     """Fills a CPU cache (oracle store) and a GPU cache (HIP store) with the same
-    seeded bf16 K/V (generated on ``gen_device``: "cuda" is faster for large
-    workloads); asserts the two caches are byte-identical."""
+    seeded K/V of ``dtype`` (bf16 or fp16; generated on ``gen_device``: "cuda"
+    is faster for large workloads); asserts the two caches are byte-identical."""
     kc_cpu, vc_cpu = wl.empty_caches("cpu")
-    wl.fill_cache(kc_cpu, vc_cpu, cpu_store, gen_device=gen_device, include_new=include_new)
+    wl.fill_cache(kc_cpu, vc_cpu, cpu_store, gen_device=gen_device, include_new=include_new, dtype=dtype)
     kc_gpu, vc_gpu = wl.empty_caches("cuda")
-    wl.fill_cache(kc_gpu, vc_gpu, store_kvcache, gen_device=gen_device, include_new=include_new)
+    wl.fill_cache(kc_gpu, vc_gpu, store_kvcache, gen_device=gen_device, include_new=include_new, dtype=dtype)
     torch.cuda.synchronize()
     assert torch.equal(kc_gpu.view(torch.uint8).cpu(), kc_cpu.view(torch.uint8)), "K cache bytes differ"
     assert torch.equal(vc_gpu.view(torch.uint8).cpu(), vc_cpu.view(torch.uint8)), "V cache bytes differ"

@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 def test_rejects_unsupported_head_dim_without_gpu():
     lib = _native.load()
     st = lib.nvamd_fp8_decode_attention(None, None, None, None, None, None, 4, 8, 2, 64, 16, 256, 4,
-                                        0.1, 0, None, 0, None)
+                                        0.1, 0, None, 0, 0, None)
     assert st == 2
     assert b"head_dim" in lib.nvamd_last_error()
 
@@ -39,30 +39,30 @@ def test_rejects_unsupported_head_dim_without_gpu():
 def test_rejects_bad_gqa_and_block_size_without_gpu():
     lib = _native.load()
     assert lib.nvamd_fp8_decode_attention(None, None, None, None, None, None, 4, 6, 4, 128, 16, 256, 4,
-                                          0.1, 0, None, 0, None) == 1
+                                          0.1, 0, None, 0, 0, None) == 1
     # block sizes must be multiples of 16 (nanovllm/config.py:30): 40 is rejected as unsupported;
     # 48 passes that check and fails later on the null pointers
     assert lib.nvamd_fp8_decode_attention(None, None, None, None, None, None, 4, 8, 2, 128, 16, 40, 4,
-                                          0.1, 0, None, 0, None) == 2
+                                          0.1, 0, None, 0, 0, None) == 2
     assert b"multiple of 16" in lib.nvamd_last_error()
     assert lib.nvamd_fp8_decode_attention(None, None, None, None, None, None, 4, 8, 2, 128, 16, 48, 4,
-                                          0.1, 0, None, 0, None) == 1
+                                          0.1, 0, None, 0, 0, None) == 1
     assert b"null pointer" in lib.nvamd_last_error()
     assert lib.nvamd_fp8_prefill_attention(None, None, None, None, None, None, None, 4, 1, 8, 2, 128, 100,
-                                           256, 2, 4, 4, 0.1, 100, None, 0, None) == 1  # part_tokens % 256
+                                           256, 2, 4, 4, 0.1, 100, None, 0, 0, None) == 1  # part_tokens % 256
     assert b"part_tokens" in lib.nvamd_last_error()
-    assert lib.nvamd_store_kvcache(None, 0, None, 0, None, None, None, -1, 8, 128, 10, None) == 1
+    assert lib.nvamd_store_kvcache(None, 0, None, 0, None, None, None, -1, 8, 128, 10, 0, None) == 1
 
 
 def test_rejects_partition_wider_than_the_block_table_window():
     """A paged split-KV partition may span at most 63 KV blocks."""
     lib = _native.load()
     st = lib.nvamd_fp8_decode_attention(None, None, None, None, None, None, 4, 8, 2, 128, 16, 256, 4,
-                                        0.1, 64 * 256, None, 0, None)
+                                        0.1, 64 * 256, None, 0, 0, None)
     assert st == 1 and b"63 blocks" in lib.nvamd_last_error()
     fake_table = 0x1000  # validation fails before any pointer is used
     st = lib.nvamd_fp8_prefill_attention(None, None, None, None, fake_table, None, None, 4, 1, 8, 2, 128,
-                                         1024, 64, 2, 4, 4, 0.1, 64 * 64, None, 0, None)
+                                         1024, 64, 2, 4, 4, 0.1, 64 * 64, None, 0, 0, None)
     assert st == 1 and b"63 blocks" in lib.nvamd_last_error()
     # the automatic choice never exceeds the window
     nb = lib.nvamd_decode_workspace_bytes(1, 8, 2, 4096, 256, 0)

@@ -106,7 +106,7 @@ def test_decode_forced_split_kv(part_tokens):
     out = torch.empty_like(qg)
     st = lib.nvamd_fp8_decode_attention(out.data_ptr(), qg.data_ptr(), gpu_c[0].data_ptr(), gpu_c[1].data_ptr(),
                                         bt.data_ptr(), ctx.data_ptr(), B, Hq, wl.num_kv_heads, 128,
-                                        wl.num_blocks, 256, nb, SCALE, part_tokens, ws.data_ptr(), ws_bytes,
+                                        wl.num_blocks, 256, nb, SCALE, part_tokens, ws.data_ptr(), ws_bytes, 0,
                                         torch.cuda.current_stream().cuda_stream)
     _native.check(st, "decode")
     torch.cuda.synchronize()
@@ -162,7 +162,7 @@ def _forced_split_decode(wl, gpu_c, qg, part_tokens):
     out = torch.empty_like(qg)
     st = lib.nvamd_fp8_decode_attention(out.data_ptr(), qg.data_ptr(), gpu_c[0].data_ptr(), gpu_c[1].data_ptr(),
                                         bt.data_ptr(), ctx.data_ptr(), B, Hq, wl.num_kv_heads, 128,
-                                        wl.num_blocks, wl.block_size, nb, SCALE, part_tokens, ws.data_ptr(), ws_bytes,
+                                        wl.num_blocks, wl.block_size, nb, SCALE, part_tokens, ws.data_ptr(), ws_bytes, 0,
                                         torch.cuda.current_stream().cuda_stream)
     _native.check(st, "decode")
     torch.cuda.synchronize()

@@ -27,7 +27,7 @@ def _decode_capi(q, kc, vc, bt, ctx, hkv, block_size, part_tokens):
     out = torch.empty_like(q)
     st = lib.nvamd_fp8_decode_attention(out.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), bt.data_ptr(),
                                         ctx.data_ptr(), B, Hq, hkv, 128, kc.shape[0], block_size, nb, SCALE,
-                                        part_tokens, ws.data_ptr(), ws_bytes,
+                                        part_tokens, ws.data_ptr(), ws_bytes, 0,
                                         torch.cuda.current_stream().cuda_stream)
     _native.check(st, "decode")
     torch.cuda.synchronize()
@@ -130,7 +130,7 @@ def test_balanced_decode_workspace_is_required():
     out = torch.empty_like(q)
     st = lib.nvamd_fp8_decode_attention(out.data_ptr(), q.data_ptr(), gpu_c[0].data_ptr(), gpu_c[1].data_ptr(),
                                         bt.data_ptr(), ctx.data_ptr(), 4, 16, 8, 128, wl.num_blocks, 256,
-                                        bt.shape[1], SCALE, 0, ws.data_ptr(), need - 1,
+                                        bt.shape[1], SCALE, 0, ws.data_ptr(), need - 1, 0,
                                         torch.cuda.current_stream().cuda_stream)
     assert st != 0 and b"workspace" in lib.nvamd_last_error()
 
@@ -155,7 +155,7 @@ def test_balanced_decode_garbage_and_reused_workspace():
         out = torch.empty_like(qg)
         st = lib.nvamd_fp8_decode_attention(out.data_ptr(), qg.data_ptr(), gpu_c[0].data_ptr(), gpu_c[1].data_ptr(),
                                             bt.data_ptr(), ctx.data_ptr(), 96, 16, 8, 128, wl.num_blocks, 256, nb,
-                                            SCALE, 0, ws.data_ptr(), need, torch.cuda.current_stream().cuda_stream)
+                                            SCALE, 0, ws.data_ptr(), need, 0, torch.cuda.current_stream().cuda_stream)
         _native.check(st, "decode")
         torch.cuda.synchronize()
         assert_close(out, want, f"garbage_ws call {call}")

@@ -141,3 +141,45 @@ def test_store_restatement_skips_padding_and_honours_row_stride():
     untouched = torch.ones(P * bs, dtype=torch.bool)
     untouched[[3, 17, 63, 0]] = False
     assert bool((kf[untouched] == 0xAB).all()) and bool((vf[untouched] == 0xCD).all())
+
+
+F16_BITS = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+F16_VALUES = F16_BITS.view(np.float16).astype(np.float32)
+
+
+def test_fp16_inputs_match_torch_cast_in_range():
+    """fp16 K/V (every pattern): the oracle's encoding of the widened value
+    against torch's own fp16 -> float8_e4m3fn cast (an independent
+    implementation) wherever torch's cast is defined the same way
+    (|x| <= 448; beyond it torch gives NaN, the reference saturates)."""
+    ok = np.abs(F16_VALUES) <= 448
+    half = torch.from_numpy(F16_BITS.view(np.int16).copy()).view(torch.float16)
+    t = half.to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    got = fp8.quantize_f16_tensor(half).numpy()
+    assert np.array_equal(got[ok], t[ok])
+    assert ok.sum() > 30000
+
+
+def test_fp16_inputs_saturate_and_keep_nan():
+    half = torch.tensor([449.0, 65504.0, -1000.0, float("inf"), float("-inf"), float("nan"), 2.0 ** -24],
+                        dtype=torch.float16)
+    got = fp8.quantize_f16_tensor(half).tolist()
+    assert got[:5] == [0x7E, 0x7E, 0xFE, 0x7E, 0xFE]
+    assert got[5] & 0x7F == 0x7F
+    assert got[6] == 0x00  # 2^-24 is far below half of the smallest subnormal (2^-10)
+
+
+def test_store_restatement_fp16_matches_bf16_on_shared_values():
+    """Values exact in both 16-bit types give the same cache bytes."""
+    Hkv, D = 2, 128
+    g = torch.Generator().manual_seed(3)
+    x = (torch.randint(-255, 256, (6, Hkv, D), generator=g).float() / 32)
+    slots = torch.tensor([5, 0, -1, 9, 2, 7], dtype=torch.int32)
+    caches = []
+    for dt in (torch.float16, torch.bfloat16):
+        kc = torch.zeros((3, 4, Hkv, D), dtype=torch.uint8)
+        vc = torch.zeros_like(kc)
+        fp8.store_kvcache(x.to(dt), (-x).to(dt), kc, vc, slots)
+        caches.append((kc, vc))
+    assert torch.equal(caches[0][0], caches[1][0]) and torch.equal(caches[0][1], caches[1][1])
+    assert int(caches[0][0].count_nonzero()) > 0

@@ -41,7 +41,7 @@ def _with_workspace(lib, wl, inputs):
                                          wl.block_size, 0)
     ws = torch.empty(max(n, 1), dtype=torch.uint8, device="cuda")
     out = torch.empty_like(q)
-    st = lib.nvamd_fp8_decode_attention(out.data_ptr(), *_args(wl, *inputs), 0, ws.data_ptr(), n,
+    st = lib.nvamd_fp8_decode_attention(out.data_ptr(), *_args(wl, *inputs), 0, ws.data_ptr(), n, 0,
                                         torch.cuda.current_stream().cuda_stream)
     _native.check(st, "nvamd_fp8_decode_attention")
     return out, n
@@ -49,7 +49,7 @@ def _with_workspace(lib, wl, inputs):
 
 def _no_alloc(lib, wl, inputs):
     out = torch.empty_like(inputs[0])
-    st = lib.nvamd_fp8_decode_attention_noalloc(out.data_ptr(), *_args(wl, *inputs),
+    st = lib.nvamd_fp8_decode_attention_noalloc(out.data_ptr(), *_args(wl, *inputs), 0,
                                                 torch.cuda.current_stream().cuda_stream)
     _native.check(st, "nvamd_fp8_decode_attention_noalloc")
     return out
@@ -88,5 +88,5 @@ def test_no_alloc_decode_rejects_shapes_beyond_the_scratch():
     assert need > lib_scratch_bytes()
     fake = 0x1000  # rejected before any pointer is used
     st = lib.nvamd_fp8_decode_attention_noalloc(fake, fake, fake, fake, fake, fake, 4096, 64, 2, 128, 20000, 256,
-                                                64, SCALE, None)
+                                                64, SCALE, 0, None)
     assert st == 3 and b"scratch" in lib.nvamd_last_error()

@@ -88,10 +88,10 @@ class PagedWorkload:
         return np.concatenate(parts) if parts else np.zeros(0, np.int32)
 
     # ---- tensors ---------------------------------------------------------
-    def make_q(self, device="cpu", seed_offset=0):
+    def make_q(self, device="cpu", seed_offset=0, dtype=torch.bfloat16):
         g = torch.Generator(device=device).manual_seed(self.seed * 1000 + 1 + seed_offset)
         return torch.randn(self.num_q_tokens(), self.num_heads, HEAD_DIM, generator=g,
-                           device=device, dtype=torch.float32).to(torch.bfloat16)
+                           device=device, dtype=torch.float32).to(dtype)
 
     def empty_caches(self, device):
         shape = (self.num_blocks, self.block_size, self.num_kv_heads, HEAD_DIM)
@@ -99,25 +99,26 @@ class PagedWorkload:
         v = torch.zeros(shape, dtype=torch.uint8, device=device)
         return k.view(torch.float8_e4m3fn), v.view(torch.float8_e4m3fn)
 
-    def kv_values(self, n_tokens, generator, device, which):
+    def kv_values(self, n_tokens, generator, device, which, dtype=torch.bfloat16):
         x = torch.randn(n_tokens, self.num_kv_heads, HEAD_DIM, generator=generator, device=device,
                         dtype=torch.float32)
         if self.outlier_frac > 0:
             mask = torch.rand(x.shape, generator=generator, device=device) < self.outlier_frac
             x = torch.where(mask, x * self.outlier_scale, x)
-        return x.to(torch.bfloat16)
+        return x.to(dtype)
 
     def fill_cache(self, k_cache, v_cache, store_fn, gen_device="cpu", include_new=True,
-                   chunk_tokens=1 << 16):
-        """Writes bf16 N(0,1) K/V for every cached key through ``store_fn``
-        (signature of store_kvcache) in chunks of ``chunk_tokens`` tokens."""
+                   chunk_tokens=1 << 16, dtype=torch.bfloat16):
+        """Writes N(0,1) K/V of ``dtype`` (bf16 or fp16) for every cached key
+        through ``store_fn`` (signature of store_kvcache) in chunks of
+        ``chunk_tokens`` tokens."""
         slots = self.cache_slots(include_new)
         g = torch.Generator(device=gen_device).manual_seed(self.seed * 1000 + 7)
         dev = k_cache.device
         for a in range(0, len(slots), chunk_tokens):
             b = min(a + chunk_tokens, len(slots))
-            kk = self.kv_values(b - a, g, gen_device, "k").to(dev)
-            vv = self.kv_values(b - a, g, gen_device, "v").to(dev)
+            kk = self.kv_values(b - a, g, gen_device, "k", dtype).to(dev)
+            vv = self.kv_values(b - a, g, gen_device, "v", dtype).to(dev)
             sm = torch.from_numpy(slots[a:b]).to(dev)
             store_fn(kk, vv, k_cache, v_cache, sm)
 
