@@ -70,12 +70,22 @@ int32_t noalloc_scratch(const char* fn, void** out) {
   return NVAMD_OK;
 }
 
+// CUs of the current device, looked up once per device (every host call
+// sizes its grid and workspace from it).
+std::atomic<int> g_cu_count[kMaxDevices];
+
 int device_cu_count() {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 256;
+  const bool cached = dev >= 0 && dev < kMaxDevices;
+  if (cached) {
+    const int n = g_cu_count[dev].load(std::memory_order_relaxed);
+    if (n > 0) return n;
+  }
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
     return 256;
+  if (cached) g_cu_count[dev].store(cus, std::memory_order_relaxed);
   return cus;
 }
 

@@ -1,7 +1,8 @@
 """ctypes binding of the gfx950 C-ABI library ``libnvamd_fp8attn.so``.
 
 The library is built in-tree by ``make -C my-nano-vllm_amd`` (see
-``__graft_entry__.build``).  There is no fallback: importing the attention
+``__graft_entry__.build``), with ``libnvamd_torch_ops.so``, the dispatcher
+operators over it (``load_ops``).  There is no fallback: importing the attention
 functions works without a GPU, but calling them without the built library
 raises ``RuntimeError``.
 
@@ -16,6 +17,9 @@ import torch  # noqa: F401  (loads torch's HIP runtime first)
 
 LIB_NAME = "libnvamd_fp8attn.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+# the torch operators over the C ABI (csrc/torch_ops.cpp), linked against LIB_NAME
+OPS_LIB_NAME = "libnvamd_torch_ops.so"
+OPS_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), OPS_LIB_NAME)
 ABI_VERSION = 6
 
 _c_void_p = ctypes.c_void_p
@@ -79,6 +83,25 @@ def load():
         raise RuntimeError(f"nanovllm_amd: ABI version {version} != expected {ABI_VERSION}; rebuild")
     _lib = lib
     return lib
+
+
+_ops_loaded = False
+
+
+def load_ops():
+    """Load (once) the torch-operator library, which registers
+    torch.ops.nvamd.store_kvcache / decode / prefill, and return
+    torch.ops.nvamd; raises if it is not built."""
+    global _ops_loaded
+    if not _ops_loaded:
+        load()  # the operators call into the C-ABI library (same file, loaded once)
+        if not os.path.exists(OPS_LIB_PATH):
+            raise RuntimeError(
+                f"nanovllm_amd: operator library {OPS_LIB_PATH} is not built; run "
+                "`make -C my-nano-vllm_amd` (or __graft_entry__.build()) first")
+        torch.ops.load_library(OPS_LIB_PATH)
+        _ops_loaded = True
+    return torch.ops.nvamd
 
 
 def check(status, what):

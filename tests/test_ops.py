@@ -49,3 +49,13 @@ def test_cpu_tensors_raise():
     with pytest.raises(NotImplementedError):
         torch.ops.nvamd.decode(q, kc, kc, torch.zeros(2, 1, dtype=torch.int32), torch.ones(2, dtype=torch.int32),
                                128 ** -0.5)
+
+
+def test_fp8_block_linear_schema_and_fake_shape():
+    assert _schema("fp8_block_linear") == ("nvamd::fp8_block_linear(Tensor x, Tensor weight, Tensor weight_scale) "
+                                           "-> Tensor")
+    m = dict(device="meta")
+    x = torch.empty(5, 256, dtype=torch.float16, **m)
+    w = torch.empty(384, 256, dtype=torch.float8_e4m3fn, **m)
+    o = torch.ops.nvamd.fp8_block_linear(x, w, torch.empty(3, 2, dtype=torch.bfloat16, **m))
+    assert o.shape == (5, 384) and o.dtype == torch.float16 and o.device.type == "meta"
