@@ -47,9 +47,10 @@ int32_t nvamd_select_logit_rows(const void* x, int64_t x_stride0, int64_t x_rows
                                 int32_t num_spec_rows, int32_t num_prefill_seqs, void* out, int64_t out_stride0,
                                 void* stream);
 
-/* Workspace needed by nvamd_sample for `rows` rows (partial results of the
- * workgroups that share a row; no initialisation needed). */
-int64_t nvamd_sample_workspace_bytes(int64_t rows);
+/* Workspace needed by nvamd_sample for `rows` rows of `vocab` logits
+ * (partial results of the workgroups that share a row; no initialisation
+ * needed). */
+int64_t nvamd_sample_workspace_bytes(int64_t rows, int64_t vocab);
 
 /*
  * Temperature sampling (sampler.py:7-12): for each row r, y = logits[r] /
@@ -58,14 +59,21 @@ int64_t nvamd_sample_workspace_bytes(int64_t rows);
  * logits[r][v] log2(e) / temperatures[r] - log2(max(E_v, 1e-10)) (the
  * softmax's max and sum do not depend on v), so two candidates whose scores
  * agree to a few ulps may be ordered differently from an fp32 softmax.  With
- * noise != NULL, E is read from it (fp32 [rows, vocab], row stride vocab);
- * otherwise E_v = -ln(((x >> 8) + 1) 2^-24) with x the word of Philox4x32-10
- * output for counter (v / 4, r, offset mod 2^32, offset >> 32) and key (seed
- * mod 2^32, seed >> 32) that belongs to element v.  logits: [rows, vocab] of
- * logits_dtype (NVAMD_LOGITS_*), row stride stride0 elements; temperatures:
- * fp32 [rows], > 0; out: int64 [rows]; workspace: 16-byte aligned,
- * nvamd_sample_workspace_bytes(rows) bytes.  vocab < 2^31 - 1
- * (NVAMD_ERR_UNSUPPORTED beyond).
+ * noise != NULL, E is read from it (fp32 [rows, vocab], row stride vocab).
+ * Otherwise the noise is drawn in the kernel from Philox4x32-10 with key
+ * (seed mod 2^32, seed >> 32), each draw x giving E = -ln(((x >> 8) + 1)
+ * 2^-24), top down by groups of 16 tokens (an exact reformulation of one
+ * Exp(1) per token, by the Gumbel-max property; the token distribution is
+ * softmax(logits / T) either way): group g = tokens [16g, 16g + 16) draws its
+ * maximum score M_g = log2(sum_v 2^(c z_v)) - log2(max(E_g, 1e-10)), c =
+ * log2(e) / T, with E_g from counter (2^31 + 64 (g / 256) + g % 64, r, offset
+ * mod 2^32, offset >> 32) word (g / 64) % 4; the first group with the largest
+ * M_g wins, and in it the first token with the largest c z_v - log2(max(E_v,
+ * 1e-10)), E_v from counter (v / 4, r, offset mod 2^32, offset >> 32) word
+ * v % 4.  logits: [rows, vocab] of logits_dtype (NVAMD_LOGITS_*), row stride
+ * stride0 elements; temperatures: fp32 [rows], > 0; out: int64 [rows];
+ * workspace: 16-byte aligned, nvamd_sample_workspace_bytes(rows, vocab)
+ * bytes.  vocab < 2^31 - 4098 (NVAMD_ERR_UNSUPPORTED beyond).
  */
 int32_t nvamd_sample(const void* logits, int32_t logits_dtype, int64_t stride0, int64_t rows, int64_t vocab,
                      const float* temperatures, const float* noise, uint64_t seed, uint64_t offset, int64_t* out,

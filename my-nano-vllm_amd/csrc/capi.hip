@@ -438,9 +438,17 @@ int32_t nvamd_select_logit_rows(const void* x, int64_t x_stride0, int64_t x_rows
                        fn);
 }
 
-int64_t nvamd_sample_workspace_bytes(int64_t rows) {
-  if (rows <= 0 || rows > 0x7fffffff) return 0;
-  return sample_parts(rows) * rows * 16;
+// Workspace of nvamd_sample: the noise path's per-part results (parts x rows
+// x (fp32 score + int64 index)) or the in-kernel path's per-quad results
+// (rows x quads x (fp32 score + int32 group)), whichever is larger.
+static int64_t sample_workspace(int64_t rows, int64_t vocab) {
+  const int64_t tasks = rows * nvamd::sample_quads(vocab);
+  return std::max<int64_t>(sample_parts(rows) * rows * 16, 2 * ((tasks * 4 + 15) & ~15ll));
+}
+
+int64_t nvamd_sample_workspace_bytes(int64_t rows, int64_t vocab) {
+  if (rows <= 0 || rows > 0x7fffffff || vocab <= 0 || vocab >= 0x7fffffff) return 0;
+  return sample_workspace(rows, vocab);
 }
 
 int32_t nvamd_sample(const void* logits, int32_t logits_dtype, int64_t stride0, int64_t rows, int64_t vocab,
@@ -451,18 +459,27 @@ int32_t nvamd_sample(const void* logits, int32_t logits_dtype, int64_t stride0, 
       logits_dtype > NVAMD_LOGITS_F32)
     return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: bad sizes or dtype (rows=%lld vocab=%lld dtype=%d)", fn,
                 (long long)rows, (long long)vocab, logits_dtype);
-  if (vocab >= 0x7fffffff)
-    return fail(NVAMD_ERR_UNSUPPORTED, "%s: vocabulary of %lld entries: at most 2^31 - 2", fn, (long long)vocab);
+  if (vocab >= 0x7fffffff - 4096)
+    return fail(NVAMD_ERR_UNSUPPORTED, "%s: vocabulary of %lld entries: at most 2^31 - 4098", fn, (long long)vocab);
   if (rows == 0) return ok();
   if (!logits || !temperatures || !out) return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+  const int64_t need = sample_workspace(rows, vocab);
+  if (workspace == nullptr || workspace_bytes < need || (uintptr_t)workspace % 16 != 0)
+    return fail(NVAMD_ERR_WORKSPACE, "%s: workspace of %lld bytes (16-byte aligned) needed", fn, (long long)need);
+  char* ws = static_cast<char*>(workspace);
+  if (noise == nullptr) {
+    const int64_t tasks = rows * nvamd::sample_quads(vocab);
+    float* task_score = reinterpret_cast<float*>(ws);
+    int* task_group = reinterpret_cast<int*>(ws + ((tasks * 4 + 15) & ~15ll));
+    return launch_status(nvamd::launch_sample_group(logits, logits_dtype, stride0, rows, vocab, temperatures, seed,
+                                                    offset, out, task_score, task_group, (hipStream_t)stream),
+                         fn);
+  }
   const int parts = sample_parts(rows);
-  if (workspace == nullptr || workspace_bytes < parts * rows * 16 || (uintptr_t)workspace % 16 != 0)
-    return fail(NVAMD_ERR_WORKSPACE, "%s: workspace of %lld bytes (16-byte aligned) needed", fn,
-                (long long)(parts * rows * 16));
-  float* part_score = static_cast<float*>(workspace);
-  int64_t* part_index = reinterpret_cast<int64_t*>(static_cast<char*>(workspace) + ((parts * rows * 4 + 15) & ~15ll));
-  return launch_status(nvamd::launch_sample(logits, logits_dtype, stride0, rows, vocab, temperatures, noise, seed,
-                                            offset, out, part_score, part_index, (int)parts, (hipStream_t)stream),
+  float* part_score = reinterpret_cast<float*>(ws);
+  int64_t* part_index = reinterpret_cast<int64_t*>(ws + ((parts * rows * 4 + 15) & ~15ll));
+  return launch_status(nvamd::launch_sample_noise(logits, logits_dtype, stride0, rows, vocab, temperatures, noise,
+                                                  out, part_score, part_index, (int)parts, (hipStream_t)stream),
                        fn);
 }
 

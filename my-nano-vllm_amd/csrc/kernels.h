@@ -129,9 +129,16 @@ hipError_t launch_build_metadata(const AttnMetaParams& p, int64_t units, hipStre
 hipError_t launch_select_rows(const void* x, int64_t x_stride_bytes, int64_t x_rows, int row_bytes,
                               const int32_t* cu_seqlens_q, int split_pt, int num_spec_rows, int num_spec_seqs,
                               int64_t out_rows, void* out, int64_t out_stride_bytes, hipStream_t stream);
-hipError_t launch_sample(const void* logits, int dtype, int64_t stride, int64_t rows, int64_t vocab,
-                         const float* temperatures, const float* noise, uint64_t seed, uint64_t offset, int64_t* out,
-                         float* part_score, int64_t* part_index, int parts, hipStream_t stream);
+// sampling with the caller's noise matrix (parts workgroups per row) ...
+hipError_t launch_sample_noise(const void* logits, int dtype, int64_t stride, int64_t rows, int64_t vocab,
+                               const float* temperatures, const float* noise, int64_t* out, float* part_score,
+                               int64_t* part_index, int parts, hipStream_t stream);
+// ... or with in-kernel noise, drawn top down by groups of 16 tokens (one
+// task per 4,096-token quad of a row: sample_quads(vocab) per row)
+int sample_quads(int64_t vocab);
+hipError_t launch_sample_group(const void* logits, int dtype, int64_t stride, int64_t rows, int64_t vocab,
+                               const float* temperatures, uint64_t seed, uint64_t offset, int64_t* out,
+                               float* task_score, int* task_group, hipStream_t stream);
 
 // FP8 block-scaled linear (128 x 128 weight blocks, 128-wide activation groups).
 struct Fp8GemmParams {

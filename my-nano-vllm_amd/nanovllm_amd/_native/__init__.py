@@ -48,7 +48,7 @@ SIGNATURES = {
                                               _c_void_p]),
     "nvamd_select_logit_rows": (_i32, [_c_void_p, _i64, _i64, _i32, _i32, _c_void_p, _i32, _i32, _i32, _i32,
                                        _c_void_p, _i64, _c_void_p]),
-    "nvamd_sample_workspace_bytes": (_i64, [_i64]),
+    "nvamd_sample_workspace_bytes": (_i64, [_i64, _i64]),
     "nvamd_sample": (_i32, [_c_void_p, _i32, _i64, _i64, _i64, _c_void_p, _c_void_p, ctypes.c_uint64,
                             ctypes.c_uint64, _c_void_p, _c_void_p, _i64, _c_void_p]),
     "nvamd_fp8_act_quant": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _i64, _i64, _c_void_p]),

@@ -4,10 +4,13 @@
 result (sampler.py:7-12): token = argmax(softmax(logits / T) / max(E, 1e-10))
 with E ~ Exp(1).  ``nvamd_sample`` computes the same argmax as that of
 logits * log2(e) / T - log2(max(E, 1e-10)) in one sweep over the logits,
-instead of the reference's fp32 copies of the whole [rows, vocab] matrix, and
-draws E in the kernel from Philox4x32-10; the generator is keyed by a seed
-taken from torch's CPU generator on every call, so ``torch.manual_seed``
-makes runs repeatable.
+instead of the reference's fp32 copies of the whole [rows, vocab] matrix.  A
+given noise matrix is used token by token; otherwise the noise is drawn in
+the kernel from Philox4x32-10, top down by groups of 16 tokens (the group's
+maximum score drawn directly, then the token inside the winning group; the
+token distribution is softmax(logits / T) either way).  The generator is
+keyed by a seed taken from torch's CPU generator on every call, so
+``torch.manual_seed`` makes runs repeatable.
 """
 import torch
 from torch import nn
@@ -39,7 +42,7 @@ def sample_tokens(logits: torch.Tensor, temperatures: torch.Tensor, noise: torch
         seed = int(torch.randint(0, 2 ** 62, (1,)).item())
     out = torch.empty(rows, dtype=torch.int64, device=logits.device)
     lib = _native.load()
-    ws_bytes = lib.nvamd_sample_workspace_bytes(rows)
+    ws_bytes = lib.nvamd_sample_workspace_bytes(rows, vocab)
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=logits.device)
     _native.check(lib.nvamd_sample(logits.data_ptr(), _DTYPE[logits.dtype], logits.stride(0), rows, vocab,
                                    temperatures.data_ptr(), noise.data_ptr() if noise is not None else None,

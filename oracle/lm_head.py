@@ -17,13 +17,24 @@
   bumped by the Weyl constants (0x9E3779B9, 0xBB67AE85).  ``exponential_noise``
   maps its output to E = -log(u), u = ((x >> 8) + 1) 2^-24 in (0, 1], with
   counter (v / 4, row, offset_lo, offset_hi) and key (seed_lo, seed_hi) for
-  elements v .. v + 3 of a row -- the stream the GPU sampler draws from.
+  elements v .. v + 3 of a row -- the token stream.
+* ``sample_grouped`` restates the GPU sampler's in-kernel draw, top down by
+  groups of 16 tokens (the Gumbel-max property: max_v (c z_v - log2 E_v) over
+  a group is itself -log2 E located at log2 sum_v 2^(c z_v), c = log2(e) / T,
+  independent of the token attaining it): group g's maximum M_g = log2 sum_v
+  2^(c z_v) - log2(max(E_g, 1e-10)) with E_g from the group stream (counter
+  (2^31 + 64 (g // 256) + g % 64, row, offset_lo, offset_hi), word
+  (g // 64) % 4), the winning group is the first argmax of M_g, and the token
+  the first argmax inside it of c z_v - log2(max(E_v, 1e-10)) on the token
+  stream.  The token distribution is softmax(z / T), as with one E per token.
 
 Pinned by tests/test_oracle_lm_head.py: Random123's published known-answer
 vectors for Philox4x32-10; torch's own CPU softmax + argmax on the same noise;
 the Gumbel-max identity argmax(p / E) = argmax(y - log E); the empirical
-distribution of samples against softmax; and the selection against torch's
-index_select of the reference's index construction.
+distribution of samples against softmax (per-token and grouped draws, the
+latter with many groups and with partial groups); the group maximum's law
+against the per-token maxima of the same groups; and the selection against
+torch's index_select of the reference's index construction.
 """
 import numpy as np
 
@@ -81,3 +92,71 @@ def sample(logits, temperatures, noise):
     p = (e / e.sum(axis=-1, keepdims=True, dtype=np.float32)).astype(np.float32)
     q = (p / np.maximum(noise, np.float32(1e-10))).astype(np.float32)
     return q.argmax(axis=-1).astype(np.int64), q
+
+
+GROUP_TOK = 16
+GROUP_COUNTER = 1 << 31
+
+
+def _uniform_exp(bits):
+    """E = -log(u), u = ((x >> 8) + 1) 2^-24, float32."""
+    u = (((bits >> np.uint64(8)) + np.uint64(1)).astype(np.float32) * np.float32(2.0 ** -24)).astype(np.float32)
+    return (-np.log(u)).astype(np.float32)
+
+
+def group_noise(seed, offset, rows, n_groups):
+    """float32 [rows, n_groups]: E_g of the group stream (module docstring)."""
+    g = np.arange(n_groups, dtype=np.uint64)[None, :].repeat(rows, 0)
+    r = np.arange(rows, dtype=np.uint64)[:, None].repeat(n_groups, 1)
+    x = np.uint64(GROUP_COUNTER) + np.uint64(64) * (g // np.uint64(256)) + g % np.uint64(64)
+    ctr = np.stack([x, r, np.full_like(g, offset & MASK32), np.full_like(g, (offset >> 32) & MASK32)], -1)
+    key = np.stack([np.full_like(g, seed & MASK32), np.full_like(g, (seed >> 32) & MASK32)], -1)
+    bits = philox4x32_10(ctr, key)
+    word = ((g // np.uint64(64)) % np.uint64(4)).astype(np.int64)
+    return _uniform_exp(np.take_along_axis(bits, word[..., None], -1)[..., 0])
+
+
+def _neg_log2_clamped(e):
+    return (-np.log2(np.maximum(e, np.float32(1e-10)))).astype(np.float32)
+
+
+def sample_grouped(logits, temperatures, seed, offset):
+    """The in-kernel draw of the GPU sampler.  logits: float array [R, V];
+    temperatures: [R].  Returns (tokens int64 [R], group scores M float32
+    [R, G], token scores float32 [R, V], filled for the tokens of each row's
+    winning group and -inf elsewhere) -- the scores let a test tell a near
+    tie from a wrong pick."""
+    z = np.asarray(logits, dtype=np.float32)
+    R, V = z.shape
+    c1 = (np.float32(1.4426950408889634) / np.asarray(temperatures, dtype=np.float32)).astype(np.float32)
+    zc = (z * c1[:, None]).astype(np.float32)
+    G = (V + GROUP_TOK - 1) // GROUP_TOK
+    pad = np.full((R, G * GROUP_TOK), -np.inf, dtype=np.float32)
+    pad[:, :V] = zc
+    zg = pad.reshape(R, G, GROUP_TOK)
+    mx = zg.max(axis=-1)
+    finite = mx > -np.inf
+    safe_mx = np.where(finite, mx, np.float32(0)).astype(np.float32)
+    s = np.zeros((R, G), dtype=np.float32)
+    with np.errstate(invalid="ignore"):
+        for i in range(GROUP_TOK):  # in token order, as the kernel sums
+            s = (s + np.exp2((zg[..., i] - safe_mx).astype(np.float32))).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        m = ((safe_mx + np.log2(s)).astype(np.float32) + _neg_log2_clamped(group_noise(seed, offset, R, G)))
+    m = np.where(finite, m, np.float32(-np.inf)).astype(np.float32)
+    gbest = m.argmax(axis=-1)
+    # token stream, drawn only for the tokens of each row's winning group
+    v = gbest[:, None].astype(np.int64) * GROUP_TOK + np.arange(GROUP_TOK)[None, :]
+    inside = v < V
+    vc = np.minimum(v, V - 1).astype(np.uint64)
+    r = np.arange(R, dtype=np.uint64)[:, None].repeat(GROUP_TOK, 1)
+    ctr = np.stack([vc // np.uint64(4), r, np.full_like(r, offset & MASK32), np.full_like(r, (offset >> 32) & MASK32)],
+                   -1)
+    key = np.stack([np.full_like(r, seed & MASK32), np.full_like(r, (seed >> 32) & MASK32)], -1)
+    bits = np.take_along_axis(philox4x32_10(ctr, key), (vc % np.uint64(4)).astype(np.int64)[..., None], -1)[..., 0]
+    sc = (np.take_along_axis(zc, np.minimum(v, V - 1), -1) + _neg_log2_clamped(_uniform_exp(bits))).astype(np.float32)
+    sc = np.where(inside, sc, np.float32(-np.inf))
+    tok_scores = np.full((R, V), -np.inf, dtype=np.float32)
+    np.put_along_axis(tok_scores, np.minimum(v, V - 1), np.where(inside, sc, tok_scores[0, 0]), -1)
+    tokens = (gbest.astype(np.int64) * GROUP_TOK + sc.argmax(axis=-1)).astype(np.int64)
+    return tokens, m, tok_scores

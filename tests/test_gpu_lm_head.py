@@ -2,12 +2,15 @@
 (nanovllm/layers/embed_head.py:56-72, nanovllm/layers/sampler.py:7-12).
 
 Selection is byte-exact.  Sampling is compared token by token with the
-oracle on the same noise (a given matrix, or the Philox4x32-10 stream the
-kernel draws in place): the tokens agree unless the oracle's two best scores
-p / E are within 1e-4 of each other (the kernel ranks by the equivalent
-log2-domain score z log2(e) / T - log2(E), whose rounding differs from the
-oracle's fp32 softmax by a few ulps).  The in-kernel noise is also checked as a
-distribution: 40,000 draws against softmax(logits / T).
+oracle on the same noise: a given matrix (the tokens agree unless the
+oracle's two best scores p / E are within 1e-4 of each other: the kernel
+ranks by the equivalent log2-domain score z log2(e) / T - log2(E), whose
+rounding differs from the oracle's fp32 softmax by a few ulps), or the
+in-kernel Philox4x32-10 draw, top down by groups of 16 tokens (the tokens
+agree unless the two groups' maxima, or the two tokens' scores inside the
+group, are within 1e-4 of each other).  The in-kernel noise is also checked
+as a distribution against softmax(logits / T): 40,000 draws of 6 logits and
+30,000 of 40 (three groups).
 """
 from dataclasses import dataclass
 
@@ -121,17 +124,42 @@ def test_sample_with_given_noise(dtype, vocab):
     _agree(got, want, q)
 
 
-def test_sample_with_in_kernel_noise_matches_the_philox_stream():
-    announce("lm head: sampler, in-kernel Philox noise, vocab 151936")
-    g = torch.Generator().manual_seed(5)
-    R, V = 40, 151936
-    logits = (torch.randn(R, V, generator=g) * 3).to(torch.bfloat16)
+def _agree_grouped(got, want, m, tok_scores, rel=1e-4):
+    G = olh.GROUP_TOK
+    bad = []
+    for r in range(len(want)):
+        if got[r] == want[r]:
+            continue
+        gg, gw = int(got[r]) // G, int(want[r]) // G
+        if gg != gw:
+            tie = abs(m[r][gg] - m[r][gw]) <= rel * max(abs(m[r][gw]), 1.0)
+        else:
+            a, b = tok_scores[r][want[r]], tok_scores[r][got[r]]
+            tie = abs(a - b) <= rel * max(abs(a), 1.0)
+        if not tie:
+            bad.append(r)
+    assert not bad, f"{len(bad)} rows differ beyond a near tie, first {bad[0]}: gpu {got[bad[0]]} oracle {want[bad[0]]}"
+
+
+@pytest.mark.parametrize("dtype,vocab,aligned", [(torch.bfloat16, 151936, True), (torch.float16, 32003, True),
+                                                 (torch.float32, 4096, True), (torch.bfloat16, 5000, False)])
+def test_sample_with_in_kernel_noise_matches_the_group_draw(dtype, vocab, aligned):
+    """The kernel's top-down draw against the oracle's, token by token; the
+    Qwen3 vocabulary, a vocabulary that leaves a partial group and a partial
+    quad, fp32 logits, and rows whose start is not 4-element aligned (the
+    element-wise load path)."""
+    announce(f"lm head: sampler, in-kernel Philox noise, {dtype}, vocab {vocab}, aligned {aligned}")
+    g = torch.Generator().manual_seed(vocab)
+    R = 40
+    full = (torch.randn(R, vocab + 1, generator=g) * 3).to(dtype)
+    logits = full[:, :vocab] if aligned else full[:, 1:]
     temps = torch.rand(R, generator=g) + 0.3
-    seed, offset = 0x1234_5678_9ABC, 77
-    got = sample_tokens(logits.cuda(), temps.cuda(), seed=seed, offset=offset).cpu().numpy()
-    noise = olh.exponential_noise(seed, offset, R, V)
-    want, q = olh.sample(logits.float().numpy(), temps.numpy(), noise)
-    _agree(got, want, q)
+    temps[0] = 1e-3                                   # nearly greedy
+    seed, offset = 0x1234_5678_9ABC + vocab, 77
+    lg = logits.cuda() if aligned else full.cuda()[:, 1:]
+    got = sample_tokens(lg, temps.cuda(), seed=seed, offset=offset).cpu().numpy()
+    want, m, tok_scores = olh.sample_grouped(logits.float().numpy(), temps.numpy(), seed, offset)
+    _agree_grouped(got, want, m, tok_scores)
 
 
 def test_in_kernel_samples_follow_softmax():
@@ -142,6 +170,22 @@ def test_in_kernel_samples_follow_softmax():
     tok = sample_tokens(logits.repeat(n, 1).cuda(), torch.full((n,), 0.7, device="cuda"), seed=2024).cpu().numpy()
     p = torch.softmax(logits / 0.7, 0).double().numpy()
     assert chisquare(np.bincount(tok, minlength=6), p * n).pvalue > 1e-4
+
+
+def test_in_kernel_samples_follow_softmax_over_groups():
+    """40 logits (groups of 16, the last partial) at T = 0.8, 30,000 draws:
+    the winning group and the token inside it together follow softmax."""
+    from scipy.stats import chisquare
+    announce("lm head: sampler distribution over three groups (30,000 draws)")
+    logits = torch.from_numpy((np.random.default_rng(40).normal(size=40) * 1.5).astype(np.float32))
+    n = 30000
+    tok = sample_tokens(logits.repeat(n, 1).cuda(), torch.full((n,), 0.8, device="cuda"), seed=77).cpu().numpy()
+    p = torch.softmax(logits.double() / 0.8, 0).numpy()
+    counts = np.bincount(tok, minlength=40)
+    big = p * n >= 20
+    obs = np.concatenate([counts[big], [counts[~big].sum()]])
+    exp = np.concatenate([p[big] * n, [p[~big].sum() * n]])
+    assert chisquare(obs, exp).pvalue > 1e-4
 
 
 def test_sampler_module_is_repeatable_under_manual_seed():

@@ -90,3 +90,61 @@ def test_select_rows_matches_the_reference_index_construction():
     got = olh.select_rows(x, split_pt, nspec, cu.tolist())
     assert torch.equal(got, want)
     assert olh.select_rows(x, split_pt, nspec, None) is x
+
+
+def _chisquare_buckets(tok, p, n, min_expected=20):
+    """Chi-square p-value of token counts against probabilities p, tokens with
+    fewer than min_expected expected draws pooled into one bucket."""
+    from scipy.stats import chisquare
+    counts = np.bincount(tok, minlength=len(p)).astype(np.float64)
+    big = p * n >= min_expected
+    obs = np.concatenate([counts[big], [counts[~big].sum()]])
+    exp = np.concatenate([p[big] * n, [p[~big].sum() * n]])
+    if exp[-1] == 0:
+        obs, exp = obs[:-1], exp[:-1]
+    return chisquare(obs, exp).pvalue
+
+
+@pytest.mark.parametrize("vocab,temp,scale,n", [(6, 0.7, 1.0, 30000), (40, 0.8, 1.5, 30000), (300, 0.5, 1.0, 30000),
+                                                (5000, 0.25, 1.0, 8000)])
+def test_grouped_draw_follows_softmax(vocab, temp, scale, n):
+    """The top-down grouped draw (groups of 16; one partial group at vocab 6,
+    40 and 300; two 4,096-token quads at 5,000) against softmax(z / T): n
+    draws (rows of the same logits), chi-square p > 1e-4 (tokens expected
+    fewer than 20 times pooled)."""
+    rng = np.random.default_rng(vocab)
+    z = (rng.normal(size=vocab) * scale).astype(np.float32)
+    tok, _, _ = olh.sample_grouped(np.tile(z, (n, 1)), np.full(n, temp, np.float32), seed=vocab * 31 + 1, offset=5)
+    y = z.astype(np.float64) / temp
+    p = np.exp(y - y.max())
+    p /= p.sum()
+    assert _chisquare_buckets(tok, p, n) > 1e-4
+
+
+def test_group_maximum_has_the_law_of_the_token_maxima():
+    """M_g, drawn directly, against max_v (c z_v - log2 E_v) over the same 16
+    tokens with one E per token (the token stream): both are Gumbel variables
+    located at log2 sum_v 2^(c z_v) (two-sample Kolmogorov-Smirnov, 20,000
+    each, p > 1e-3; a dropped log2-sum or a wrong sign shifts one by a full
+    unit)."""
+    from scipy.stats import ks_2samp
+    rng = np.random.default_rng(3)
+    z = (rng.normal(size=16) * 2).astype(np.float32)
+    n = 20000
+    _, m, tok_scores = olh.sample_grouped(np.tile(z, (n, 1)), np.ones(n, np.float32), seed=11, offset=0)
+    direct = m[:, 0].astype(np.float64)
+    per_token = tok_scores.max(axis=1).astype(np.float64)
+    assert ks_2samp(direct, per_token).pvalue > 1e-3
+    loc = np.log2(np.exp2(z.astype(np.float64) * 1.4426950408889634).sum())
+    # Gumbel in log2 units: mean = loc + Euler-Mascheroni / ln 2
+    assert abs(direct.mean() - (loc + 0.5772156649 / np.log(2))) < 0.03
+
+
+def test_group_and_token_streams_are_distinct():
+    """The group stream's counters start at 2^31, above every token counter
+    (v / 4 < 2^29): the two draws of a row never share a Philox output."""
+    e_tok = olh.exponential_noise(seed=5, offset=9, rows=2, vocab=64 * 4)
+    e_grp = olh.group_noise(seed=5, offset=9, rows=2, n_groups=64)
+    assert not np.isin(e_grp, e_tok).any()
+    again = olh.group_noise(seed=5, offset=9, rows=2, n_groups=64)
+    assert np.array_equal(e_grp, again) and e_grp.min() > 0
