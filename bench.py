@@ -312,17 +312,19 @@ def bench_contiguous_batch(wl, pools, q, steps, warmup):
 FP8_PEAK_TFLOPS = 5000.0       # MI355X dense FP8 MFMA
 
 
-def bench_fp8_linear(M, N, K, steps, warmup, n_weights=2):
+def bench_fp8_linear(M, N, K, steps, warmup):
     """The FP8 block-scaled linear layer at one shape: the GEMM alone (on
     already-quantised activations, the reference's second kernel), the
     activation quantisation alone, and fp8_block_linear end to end.  Random
-    finite E4M3FN weights; n_weights copies are cycled so that the decode-size
-    GEMM streams its weights from HBM."""
+    finite E4M3FN weights; copies totalling more than 600 MiB are cycled, so
+    the weights stream from HBM as in a model step (which reads every layer's
+    weights once) and not from the 256 MB last-level cache."""
     from nanovllm_amd import _native
     from nanovllm_amd.kernels.fp8_linear import fp8_block_linear
     lib = _native.load()
     g = torch.Generator(device="cuda").manual_seed(M + N + K)
     x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    n_weights = max(2, -(-(600 << 20) // (N * K)))
     ws = []
     for _ in range(n_weights):
         c = torch.randint(0, 256, (N, K), device="cuda", generator=g, dtype=torch.int32).to(torch.uint8)
@@ -333,11 +335,14 @@ def bench_fp8_linear(M, N, K, steps, warmup, n_weights=2):
     out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
     stream = torch.cuda.current_stream().cuda_stream
     _native.check(lib.nvamd_fp8_act_quant(x.data_ptr(), K, 0, xq.data_ptr(), xs.data_ptr(), M, K, stream), "quant")
+    gws_n = lib.nvamd_fp8_block_gemm_workspace_bytes(M, N, K)
+    gws = torch.empty(max(gws_n, 16), dtype=torch.uint8, device="cuda")
 
     def gemm(i):
         w = ws[i % n_weights]
         _native.check(lib.nvamd_fp8_block_gemm(xq.data_ptr(), xs.data_ptr(), w.data_ptr(), K, w_scale.data_ptr(),
-                                               out.data_ptr(), N, 0, M, N, K, stream), "gemm")
+                                               out.data_ptr(), N, 0, M, N, K, gws.data_ptr(), gws_n, stream),
+                      "gemm")
 
     def quant(i):
         _native.check(lib.nvamd_fp8_act_quant(x.data_ptr(), K, 0, xq.data_ptr(), xs.data_ptr(), M, K, stream), "quant")
@@ -888,8 +893,10 @@ def main():
                 + f"); hipBLASLt per-tensor {r['hipblaslt_per_tensor_us']} us")
         extra["fp8_linear"] = dict(
             workload="FP8 block-scaled linear (128x128 weight blocks), Qwen3-8B shapes",
-            kernels="block_gemm_kernel (act_quant_kernel timed separately); hipblaslt_per_tensor_us: "
-                    "torch._scaled_mm with one scale per tensor, same operands", **lin)
+            kernels="block_gemm_kernel; skinny_gemm_kernel (+ skinny_reduce_kernel when K is split) for at most "
+                    "256 tokens where the tile grid would leave CUs idle; act_quant_kernel timed separately; "
+                    "hipblaslt_per_tensor_us: torch._scaled_mm with one scale per tensor, same operands; weights "
+                    "cycled over > 600 MiB (streamed from HBM)", **lin)
         if not args.no_cpu_baseline:
             log("cpu baseline (oracle) for the FP8 linear")
             extra["fp8_linear"]["cpu_baseline"] = cpu_baseline_fp8_linear(6144, 4096)

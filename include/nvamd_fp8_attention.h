@@ -58,7 +58,7 @@ extern "C" {
 #define NVAMD_DTYPE_F16 1
 
 /* ABI version of this header and nvamd_fp8_linear.h (bumped on any signature change). */
-#define NVAMD_ABI_VERSION 6
+#define NVAMD_ABI_VERSION 7
 int32_t nvamd_abi_version(void);
 
 /* Description of the last error on the calling thread ("" if none). */

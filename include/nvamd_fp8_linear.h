@@ -57,10 +57,22 @@ int32_t nvamd_fp8_act_quant(const void* x, int64_t x_stride0, int32_t x_dtype, v
  *   accumulation, rounded to out_dtype (RNE).
  * Pointers 16-byte aligned (out 8).  K is limited by the LDS that holds a
  * tile's scales: NVAMD_ERR_UNSUPPORTED beyond it (K <= 32768 always fits).
+ *
+ * workspace (16-byte aligned, contents ignored; NULL with workspace_bytes 0
+ * allowed): M <= 256 tokens take a kernel that streams each weight row once
+ * and may split K over workgroups; it then writes fp32 partial sums there and
+ * adds them in split order (repeated calls are bit-identical).  With less
+ * than nvamd_fp8_block_gemm_workspace_bytes(M, N, K) bytes, K is split only
+ * as far as the workspace holds.  The reference's launch has no workspace: its
+ * grid tiles (M, N) only (fp8_linear.py:125-138).
  */
 int32_t nvamd_fp8_block_gemm(const void* xq, const void* x_scale, const void* weight, int64_t weight_stride0,
                              const void* weight_scale, void* out, int64_t out_stride0, int32_t out_dtype, int64_t M,
-                             int64_t N, int64_t K, void* stream);
+                             int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes nvamd_fp8_block_gemm uses for an M x N x K product on the
+ * current device (0: none). */
+int64_t nvamd_fp8_block_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
 #ifdef __cplusplus
 }

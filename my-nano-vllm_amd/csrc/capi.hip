@@ -320,9 +320,26 @@ int32_t nvamd_fp8_act_quant(const void* x, int64_t x_stride0, int32_t x_dtype, v
                        fn);
 }
 
+namespace {
+
+int64_t device_lds_limit() {
+  int dev = 0, lds_limit = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&lds_limit, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || lds_limit <= 0)
+    lds_limit = 160 * 1024;
+  return lds_limit;
+}
+
+}  // namespace
+
+int64_t nvamd_fp8_block_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0 || N % 128 != 0 || K % 128 != 0 || N > 0x7fffffffll || K > 0x7fffffffll) return 0;
+  return nvamd::fp8_skinny_workspace_bytes(M, N, (int)(K / 128), device_cu_count(), device_lds_limit());
+}
+
 int32_t nvamd_fp8_block_gemm(const void* xq, const void* x_scale, const void* weight, int64_t weight_stride0,
                              const void* weight_scale, void* out, int64_t out_stride0, int32_t out_dtype, int64_t M,
-                             int64_t N, int64_t K, void* stream) {
+                             int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, void* stream) {
   static const char* fn = "fp8_block_gemm";
   if (M < 0 || N <= 0 || K <= 0 || N % 128 != 0 || K % 128 != 0 || weight_stride0 < K || out_stride0 < N ||
       N > 0x7fffffffll || K > 0x7fffffffll)
@@ -331,6 +348,11 @@ int32_t nvamd_fp8_block_gemm(const void* xq, const void* x_scale, const void* we
   if (out_dtype != NVAMD_DTYPE_BF16 && out_dtype != NVAMD_DTYPE_F16)
     return fail(NVAMD_ERR_UNSUPPORTED, "%s: out_dtype must be bf16 or fp16 (got %d)", fn, out_dtype);
   if (M == 0) return ok();
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && workspace == nullptr))
+    return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: workspace_bytes=%lld with a null workspace", fn,
+                (long long)workspace_bytes);
+  if ((uintptr_t)workspace % 16 != 0)
+    return fail(NVAMD_ERR_UNSUPPORTED, "%s: workspace must be 16-byte aligned", fn);
   if (!xq || !x_scale || !weight || !weight_scale || !out) return fail(NVAMD_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
   if ((uintptr_t)xq % 16 != 0 || (uintptr_t)x_scale % 16 != 0 || (uintptr_t)weight % 16 != 0 ||
       weight_stride0 % 16 != 0 || (uintptr_t)weight_scale % 16 != 0 || (uintptr_t)out % 8 != 0 || out_stride0 % 4 != 0)
@@ -340,12 +362,10 @@ int32_t nvamd_fp8_block_gemm(const void* xq, const void* x_scale, const void* we
                 fn);
   if (weight_stride0 * 256 > 0xffffffffll || M * K > (1ll << 46))
     return fail(NVAMD_ERR_UNSUPPORTED, "%s: weight row stride or activation size beyond 32-bit tile offsets", fn);
-  int dev = 0, lds_limit = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&lds_limit, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || lds_limit <= 0)
-    lds_limit = 160 * 1024;
+  const int64_t lds_limit = device_lds_limit();
   const int Kc = (int)(K / 128);
-  const int config = nvamd::fp8_gemm_pick_config(M, N, Kc, device_cu_count(), lds_limit);
+  const nvamd::SkinnyPlan plan = nvamd::fp8_skinny_plan(M, N, Kc, device_cu_count(), workspace_bytes, lds_limit);
+  const int config = plan.cw > 0 ? 0 : nvamd::fp8_gemm_pick_config(M, N, Kc, device_cu_count(), lds_limit);
   if (config < 0)
     return fail(NVAMD_ERR_UNSUPPORTED, "%s: K=%lld needs more LDS for the tile scales than the device has", fn,
                 (long long)K);
@@ -361,6 +381,10 @@ int32_t nvamd_fp8_block_gemm(const void* xq, const void* x_scale, const void* we
   p.N = (int)N;
   p.K = (int)K;
   p.Kc = Kc;
+  if (plan.cw > 0)
+    return launch_status(nvamd::launch_fp8_skinny_gemm(p, plan, out_dtype == NVAMD_DTYPE_F16,
+                                                       static_cast<float*>(workspace), (hipStream_t)stream),
+                         fn);
   return launch_status(nvamd::launch_fp8_block_gemm(p, config, out_dtype == NVAMD_DTYPE_F16, (hipStream_t)stream), fn);
 }
 

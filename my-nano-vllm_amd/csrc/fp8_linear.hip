@@ -34,7 +34,10 @@
 // in both operands, so any assignment of K positions to (lane, byte) that
 // the hardware uses for A it also uses for B, and the sum over K is exact
 // up to the MFMA's own fp32 accumulation.
+#include <algorithm>
 #include <atomic>
+#include <climits>
+#include <cmath>
 
 #include "fp8_common.h"
 #include "kernels.h"
@@ -130,13 +133,20 @@ int64_t gemm_lds_bytes(int Kc) {
   return 2 * T::kStage + round_up_1k(((int64_t)T::kWBlocks * Kc + 8) * 2);
 }
 
+// Granule swizzle of a staged 128-byte row r: granule g sits at position
+// g ^ frag_swz(r).  A fragment read takes one granule from each of 16 rows
+// (the same g); a 16-byte read of row r at position p covers banks
+// 4p + 32 (r & 1) .. + 3, so the 16 rows hit 16 distinct bank groups when the
+// even rows, and the odd rows, take 8 distinct positions: (r >> 1) & 7.
+// ((r & 7) would put rows r and r + 8 on the same banks.)
+__device__ __forceinline__ int frag_swz(int r) { return (r >> 1) & 7; }
+
 // 8 swizzled fragment bytes -> MFMA operand: row r (16 rows), K-chunk q =
-// lane / 16 (32 bytes = granules 2q, 2q + 1 at positions (2q) ^ (r & 7),
-// (2q + 1) ^ (r & 7) of the row's 128 bytes).
+// lane / 16 (32 bytes = granules 2q, 2q + 1 of the row's 128 bytes).
 __device__ __forceinline__ i32x8 read_frag(const uint8_t* rows, int r, int q) {
   const uint8_t* row = rows + r * kFp8Block;
-  const u32x4 a = *reinterpret_cast<const u32x4*>(row + 16 * ((2 * q) ^ (r & 7)));
-  const u32x4 b = *reinterpret_cast<const u32x4*>(row + 16 * ((2 * q + 1) ^ (r & 7)));
+  const u32x4 a = *reinterpret_cast<const u32x4*>(row + 16 * ((2 * q) ^ frag_swz(r)));
+  const u32x4 b = *reinterpret_cast<const u32x4*>(row + 16 * ((2 * q + 1) ^ frag_swz(r)));
   return i32x8{(int)a.x, (int)a.y, (int)a.z, (int)a.w, (int)b.x, (int)b.y, (int)b.z, (int)b.w};
 }
 
@@ -167,15 +177,15 @@ __global__ __launch_bounds__(64 * WN * WM) void block_gemm_kernel(Fp8GemmParams 
 
   // fetch offsets: load i of this wave covers tile rows 8 (wave + kWaves i) ..
   // + 7; lane l -> row + l / 8, LDS granule position l % 8, global granule
-  // (l % 8) ^ (row & 7)
+  // (l % 8) ^ frag_swz(row)
   const int fr = lane >> 3, fp = lane & 7;
   auto w_off = [&](int i, int kc) {
     const int r = 8 * (wave + T::kWaves * i) + fr;
-    return (uint32_t)((int64_t)r * p.w_stride + kc * kFp8Block + 16 * (fp ^ (r & 7)));
+    return (uint32_t)((int64_t)r * p.w_stride + kc * kFp8Block + 16 * (fp ^ frag_swz(r)));
   };
   auto x_off = [&](int i, int kc) {
     const int r = 8 * (wave + T::kWaves * i) + fr;
-    return (uint32_t)((int64_t)r * Kc * kFp8Block + kc * kFp8Block + 16 * (fp ^ (r & 7)));
+    return (uint32_t)((int64_t)r * Kc * kFp8Block + kc * kFp8Block + 16 * (fp ^ frag_swz(r)));
   };
   // wave w < kSxLoads: token rows 64 w + lane, the dword holding x_scale[row][kc]
   const uint32_t sx_row_off = (uint32_t)((64 * wave + lane) * Kc) * 2u;
@@ -258,6 +268,235 @@ __global__ __launch_bounds__(64 * WN * WM) void block_gemm_kernel(Fp8GemmParams 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Skinny GEMM (M <= 256 tokens): the weights stream once, into registers
+// ---------------------------------------------------------------------------
+// With few tokens the weights are nearly all of the bytes (Qwen3-8B gate/up
+// at 192 tokens: 100.7 MB of weights, 0.8 MB of activations), and a tile grid
+// over (features, tokens) re-reads them per token tile, reads each row 128
+// bytes at a time (one K block per stage) and waits for every stage at a
+// barrier.  Here a workgroup owns BN = 16 CW features, all tokens (16 MF rows)
+// and a range of K blocks, on CW compute waves and LW loader waves:
+//  - compute wave w owns features n0 + 16 w .. + 15 and loads its weight rows
+//    straight into registers, four K blocks (512 bytes of each row) per batch,
+//    two batches in flight; its only vector-memory loads are these, so the
+//    compiler's wait counts for them are exact and no barrier waits for them;
+//  - the loader waves stage the activation rows of a K block and, per token
+//    row, the x_scale dword of the block (direct-to-LDS loads) in a ring of
+//    kStages stages, one barrier per K block;
+//  - per K block a compute wave runs MF MFMAs (its weight fragment against
+//    each 16-token fragment) and the block-scale FMAs.
+// A lane feeds the MFMA granules q and q + 4 (q = lane / 16) of its row in
+// both operands, so the K positions pair up whatever the hardware's lane
+// layout, and each weight load instruction reads 64 contiguous bytes of 16
+// rows.  With one K range (splits = 1) the workgroup rounds and stores the
+// output; otherwise it stores fp32 partial sums to the workspace, [split][M][N],
+// and skinny_reduce_kernel adds them in split order (bit-identical on repeat).
+constexpr int kSkinnyBatch = 4;  // K blocks per weight batch
+
+template <int CW, int MF>
+struct Skinny {
+  static constexpr int LW = MF >= 12 ? 2 : 1;            // loader waves
+  static constexpr int kWaves = CW + LW;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int BN = 16 * CW;
+  static constexpr int kRows = 16 * MF;                  // token rows of a stage
+  static constexpr int kXBytes = kRows * kFp8Block;      // activation rows of one K block
+  static constexpr int kXLoads = kXBytes / 1024;         // 1 KiB loads, 8 rows each
+  static constexpr int kSxLoads = (kRows + 63) / 64;     // dword loads, 64 rows each
+  static constexpr int kStage = kXBytes + 256 * kSxLoads;
+  // loader l issues activation loads l, l + LW, ... and, if l == 0, the scale loads
+  static constexpr int kLoads0 = (kXLoads + LW - 1) / LW + kSxLoads;
+  static constexpr int kLoads1 = kXLoads / LW;
+  // stages in the ring: kStages - 1 in flight per loader within vmcnt's 63
+  static constexpr int kStages = 1 + 63 / kLoads0 < 4 ? 1 + 63 / kLoads0 : 4;
+  static_assert(kXLoads % LW == 0, "activation loads split evenly over the loaders");
+  static_assert(kStages >= 2, "at least one stage in flight");
+  static_assert(BN <= kFp8Block && kFp8Block % BN == 0, "a workgroup's features lie in one weight block");
+};
+
+// LDS bytes of a skinny launch: the ring, then the weight scales of the
+// workgroup's K range (bf16, from up to 7 elements earlier, whole 1 KiB loads).
+template <int CW, int MF>
+int64_t skinny_lds_bytes(int kper) {
+  using T = Skinny<CW, MF>;
+  return (int64_t)T::kStages * T::kStage + round_up_1k(((int64_t)kper + 8) * 2);
+}
+
+// Fragment bytes for the skinny kernel: granules q and q + 4 of row r.
+__device__ __forceinline__ i32x8 read_frag_split(const uint8_t* rows, int r, int q) {
+  const uint8_t* row = rows + r * kFp8Block;
+  const u32x4 a = *reinterpret_cast<const u32x4*>(row + 16 * (q ^ frag_swz(r)));
+  const u32x4 b = *reinterpret_cast<const u32x4*>(row + 16 * ((q + 4) ^ frag_swz(r)));
+  return i32x8{(int)a.x, (int)a.y, (int)a.z, (int)a.w, (int)b.x, (int)b.y, (int)b.z, (int)b.w};
+}
+
+template <int CW, int MF, bool PARTIAL>
+__global__ __launch_bounds__((64 * Skinny<CW, MF>::kWaves)) void skinny_gemm_kernel(Fp8GemmParams p, int kper,
+                                                                                 float* __restrict__ part,
+                                                                                 int f16_out) {
+  using T = Skinny<CW, MF>;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const uint32_t lds0 = wave_uniform((int)lds_addr(smem));
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_uniform(tid >> 6);
+  const int n0 = (int)blockIdx.x * T::BN;
+  const int split = (int)blockIdx.y;
+  const int Kc = p.Kc;
+  const int kc0 = split * kper, kc1 = min(Kc, kc0 + kper);
+  const int nk = kc1 - kc0;  // >= 1: the launch has no empty splits
+  const int64_t sw_first = (int64_t)(n0 / kFp8Block) * Kc + kc0;
+  const int sw_shift = (int)(sw_first & 7);
+  const uint32_t sw_off = (uint32_t)(T::kStages * T::kStage);
+  const uint16_t* sw_lds = reinterpret_cast<const uint16_t*>(smem + sw_off) + sw_shift;
+
+  if (wave >= CW) {
+    // ---- loader waves ------------------------------------------------------
+    const int l = wave - CW;
+    const u32x4 rx = rsrc_words(p.xq, (uint32_t)(p.M * p.K));
+    const u32x4 rsx = rsrc_words(p.x_scale, (uint32_t)((p.M * Kc * 2 + 3) & ~3ll));
+    if (l == 0) {
+      const u32x4 rsw = rsrc_words(p.w_scale + (sw_first - sw_shift), (uint32_t)(((int64_t)nk + sw_shift) * 2 + 3) & ~3u);
+      for (int i = 0; i < (int)(round_up_1k(((int64_t)kper + 8) * 2) / 1024); ++i)
+        dma_load16_keep(rsw, 1024u * i + 16u * lane, lds0 + sw_off + 1024u * i);
+    }
+    const int fr = lane >> 3, fp = lane & 7;
+    // Stage kc into slot s.  Stages past the range are issued too (their
+    // bytes are never read), so every wait below counts the same loads.
+    auto issue_stage = [&](int kc, int s) {
+      const uint32_t base = lds0 + (uint32_t)(s * T::kStage);
+#pragma unroll
+      for (int i0 = 0; i0 < T::kXLoads; i0 += T::LW) {
+        const int i = i0 + l;
+        const int r = 8 * i + fr;
+        dma_load16_keep(rx, (uint32_t)r * (uint32_t)p.K + (uint32_t)kc * kFp8Block + 16u * (uint32_t)(fp ^ frag_swz(r)),
+                        base + 1024u * i);
+      }
+      if (l == 0) {
+#pragma unroll
+        for (int i = 0; i < T::kSxLoads; ++i) {
+          const int r = 64 * i + lane;
+          dma_load4_keep(rsx, ((uint32_t)(r * Kc + kc) * 2u) & ~3u, base + (uint32_t)(T::kXBytes + 256 * i));
+        }
+      }
+    };
+#pragma unroll
+    for (int t = 0; t < T::kStages - 1; ++t) issue_stage(kc0 + t, t);
+    const int nk_pad = (nk + 2 * kSkinnyBatch - 1) / (2 * kSkinnyBatch) * (2 * kSkinnyBatch);  // the compute rounds
+    for (int k = 0; k < nk_pad; ++k) {
+      // stage k has landed once at most the kStages - 2 later stages are in flight
+      if (l == 0) wait_vmcnt<(T::kStages - 2) * T::kLoads0>();
+      else wait_vmcnt<(T::kStages - 2) * T::kLoads1>();
+      lds_barrier();  // publishes stage k; every compute wave is done with stage k - 1
+      issue_stage(kc0 + k + T::kStages - 1, (k + T::kStages - 1) % T::kStages);
+    }
+    wait_vmcnt<0>();  // nothing may land in LDS after the workgroup exits
+    return;
+  }
+
+  // ---- compute waves -------------------------------------------------------
+  const int q = lane >> 4, r16 = lane & 15;
+  const __amdgpu_buffer_rsrc_t rw =
+      make_rsrc(p.w + (int64_t)(n0 + 16 * wave) * p.w_stride, (uint32_t)(16 * p.w_stride));
+  const uint32_t w_row = (uint32_t)r16 * (uint32_t)p.w_stride + 16u * (uint32_t)q;
+  u32x4 wr[2][kSkinnyBatch][2];  // two batches of kSkinnyBatch K blocks, granules q and q + 4
+  // Batch b <- K blocks kc .. kc + 3; blocks past the range re-read its last
+  // block (unconditional loads keep the compiler's wait counts exact).
+  auto load_batch = [&](int b, int kc) {
+#pragma unroll
+    for (int u = 0; u < kSkinnyBatch; ++u) {
+      const uint32_t off = w_row + (uint32_t)min(kc + u, kc1 - 1) * kFp8Block;
+      wr[b][u][0] = buf_load16(rw, off);
+      wr[b][u][1] = buf_load16(rw, off + 64u);
+      // issued in block order everywhere (the prologue too), so the compiler's
+      // count of younger loads is the same on every path into the loop
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  f32x4 acc[MF];
+#pragma unroll
+  for (int j = 0; j < MF; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  load_batch(0, kc0);
+  load_batch(1, kc0 + kSkinnyBatch);
+
+  // The loop body is straight-line over 2 kSkinnyBatch blocks (branches in
+  // it make the compiler drain every load in flight): blocks k >= nk of the
+  // last round use the range's last weight block and the next activation
+  // stages with a zero scale, which adds +0 (every operand is finite).
+  for (int k0 = 0; k0 < nk; k0 += 2 * kSkinnyBatch) {
+#pragma unroll
+    for (int t = 0; t < 2 * kSkinnyBatch; ++t) {
+      const int k = k0 + t;
+      lds_barrier();  // stage k is in LDS
+      const uint8_t* st = smem + (k % T::kStages) * T::kStage;
+      const uint32_t* sx_dw = reinterpret_cast<const uint32_t*>(st + T::kXBytes);
+      float sw = bf16_bits_to_f32(sw_lds[min(k, nk - 1)]);
+      asm volatile("" : "+v"(sw));  // read in every block (no branch around it)
+      sw = k < nk ? sw : 0.f;
+      const u32x4 lo = wr[t / kSkinnyBatch][t % kSkinnyBatch][0], hi = wr[t / kSkinnyBatch][t % kSkinnyBatch][1];
+      const i32x8 a = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+      const int kc = kc0 + k;
+#pragma unroll
+      for (int j = 0; j < MF; ++j) {
+        const int row = 16 * j + r16;
+        const uint32_t d = sx_dw[row];
+        const float s = bf16_bits_to_f32((row * Kc + kc) & 1 ? d >> 16 : d & 0xFFFFu) * sw;  // exact
+        const i32x8 b = read_frag_split(st + 16 * j * kFp8Block, r16, q);
+        const f32x4 pr = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0,
+                                                                          127, 0, 127);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[j][e] = __builtin_fmaf(pr[e], s, acc[j][e]);
+      }
+      // The block's MFMAs stay before the next barrier (the compiler would
+      // sink them all to the end of the unrolled body, every block's operands
+      // live at once) and the refill after the batch's last use.
+#pragma unroll
+      for (int j = 0; j < MF; ++j) asm volatile("" : "+v"(acc[j]));
+      __builtin_amdgcn_sched_barrier(0);
+      if (t % kSkinnyBatch == kSkinnyBatch - 1)
+        load_batch(t / kSkinnyBatch, kc0 + k0 + t + 1 + kSkinnyBatch);  // refill the batch just used
+    }
+  }
+
+  // lane holds D[4q + e][r16] of fragment j: token 16 j + r16, features
+  // n0 + 16 wave + 4q .. + 3
+  const int nf = n0 + 16 * wave + 4 * q;
+#pragma unroll
+  for (int j = 0; j < MF; ++j) {
+    const int64_t m = 16 * j + r16;
+    if (m >= p.M) continue;
+    const f32x4 v = acc[j];
+    if (PARTIAL) {
+      *reinterpret_cast<f32x4*>(part + ((int64_t)split * p.M + m) * p.N + nf) = v;
+    } else {
+      const u32x2 o = f16_out ? u32x2{pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3])}
+                              : u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+      *reinterpret_cast<u32x2*>(p.out + m * p.out_stride + nf) = o;
+    }
+  }
+}
+
+// out[m, n .. n + 3] = round(sum over splits s, in order, of part[s][m][n .. n + 3]);
+// one thread per four outputs.
+__global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restrict__ part, int splits, int64_t M,
+                                                            int N, uint16_t* __restrict__ out, int64_t out_stride,
+                                                            int f16_out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t per_row = N / 4;
+  if (i >= M * per_row) return;
+  const int64_t m = i / per_row;
+  const int n = (int)(i - m * per_row) * 4;
+  const int64_t plane = M * N;
+  const float* src = part + m * N + n;
+  f32x4 v = *reinterpret_cast<const f32x4*>(src);
+  for (int s = 1; s < splits; ++s) {
+    const f32x4 t = *reinterpret_cast<const f32x4*>(src + s * plane);
+    v = f32x4{v[0] + t[0], v[1] + t[1], v[2] + t[2], v[3] + t[3]};
+  }
+  const u32x2 o = f16_out ? u32x2{pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3])}
+                          : u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+  *reinterpret_cast<u32x2*>(out + m * out_stride + n) = o;
+}
+
 // Tile configurations, largest first: (WN, WM, TN, TM) -> BN x BM.
 //   0: 2 x 4 waves, 8 x 4 fragments -> 256 features x 256 tokens (one
 //      workgroup of 8 waves per CU: a K block is ~1 us of MFMA work, about
@@ -296,7 +535,130 @@ hipError_t launch_config(const Fp8GemmParams& p, int64_t lds, hipStream_t stream
   return hipGetLastError();
 }
 
+template <int CW, int MF, bool PARTIAL>
+hipError_t launch_skinny_kernel(const Fp8GemmParams& p, int splits, int kper, bool f16_out, float* part,
+                                hipStream_t stream) {
+  using T = Skinny<CW, MF>;
+  auto kern = skinny_gemm_kernel<CW, MF, PARTIAL>;
+  const int64_t lds = skinny_lds_bytes<CW, MF>(kper);
+  static std::atomic<int64_t> lds_set{0};  // largest dynamic LDS size granted so far
+  if (lds > lds_set.load(std::memory_order_relaxed)) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)lds);
+    if (e != hipSuccess) return e;
+    lds_set.store(lds, std::memory_order_relaxed);
+  }
+  const dim3 grid((unsigned)(p.N / T::BN), (unsigned)splits);
+  hipLaunchKernelGGL(kern, grid, dim3(T::kThreads), (size_t)lds, stream, p, kper, part, f16_out ? 1 : 0);
+  return hipGetLastError();
+}
+
+template <int CW, int MF>
+hipError_t launch_skinny_t(const Fp8GemmParams& p, int splits, int kper, bool f16_out, float* part,
+                           hipStream_t stream) {
+  if (splits == 1) return launch_skinny_kernel<CW, MF, false>(p, 1, kper, f16_out, nullptr, stream);
+  hipError_t e = launch_skinny_kernel<CW, MF, true>(p, splits, kper, f16_out, part, stream);
+  if (e != hipSuccess) return e;
+  const int64_t threads = p.M * (p.N / 4);
+  hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, part,
+                     splits, p.M, p.N, p.out, p.out_stride, f16_out ? 1 : 0);
+  return hipGetLastError();
+}
+
+// Instances: CW 8 only up to MF 12 (beyond it 10 waves leave too few registers).
+constexpr bool skinny_has(int cw, int mf) { return cw != 8 || mf <= 12; }
+
+template <int CW>
+hipError_t launch_skinny_cw(const Fp8GemmParams& p, int mf, int splits, int kper, bool f16_out, float* part,
+                            hipStream_t stream) {
+  switch (mf) {
+    case 1: return launch_skinny_t<CW, 1>(p, splits, kper, f16_out, part, stream);
+    case 2: return launch_skinny_t<CW, 2>(p, splits, kper, f16_out, part, stream);
+    case 4: return launch_skinny_t<CW, 4>(p, splits, kper, f16_out, part, stream);
+    case 8: return launch_skinny_t<CW, 8>(p, splits, kper, f16_out, part, stream);
+    default:
+      if constexpr (skinny_has(CW, 12)) {
+        if (mf == 12) return launch_skinny_t<CW, 12>(p, splits, kper, f16_out, part, stream);
+        if (mf == 16) return launch_skinny_t<CW, 16>(p, splits, kper, f16_out, part, stream);
+      }
+      return hipErrorInvalidValue;
+  }
+}
+
+int64_t skinny_lds(int cw, int mf, int kper) {
+  // the ring does not depend on CW
+  (void)cw;
+  switch (mf) {
+    case 1: return skinny_lds_bytes<2, 1>(kper);
+    case 2: return skinny_lds_bytes<2, 2>(kper);
+    case 4: return skinny_lds_bytes<2, 4>(kper);
+    case 8: return skinny_lds_bytes<2, 8>(kper);
+    case 12: return skinny_lds_bytes<2, 12>(kper);
+    default: return skinny_lds_bytes<2, 16>(kper);
+  }
+}
+
 }  // namespace
+
+SkinnyPlan fp8_skinny_plan(int64_t M, int64_t N, int Kc, int cus, int64_t workspace_bytes, int64_t lds_limit) {
+  SkinnyPlan best;
+  if (M < 1 || M > kSkinnyMaxM || N % 128 != 0 || Kc < 1 || (int64_t)Kc * kFp8Block >= (1 << 24) || cus < 1)
+    return best;
+  // A tile grid that covers the CUs keeps them busier (measured at 192
+  // tokens: gate/up, 576 tiles of 128 x 64, 41.8 us against 50 us here); the
+  // small-M kernel is for grids that would leave CUs idle (qkv 144 tiles:
+  // 27.3 -> 24.3 us; down 96 tiles: 63.7 -> 35.3 us, weights streamed from
+  // HBM).
+  if ((N / 128) * ((M + 63) / 64) >= cus) return best;
+  const int mf = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : M <= 128 ? 8 : M <= 192 ? 12 : 16;
+  // Estimated time (us): a workgroup's K blocks are latency-bound, about
+  // 0.40 + 0.19 CW us each at 192 tokens (less with fewer token fragments),
+  // one round of workgroups per CU; a split adds the partial sums' HBM writes
+  // and reads and the reduce launch (about 3 us + 2 x bytes / 5 TB/s).
+  double best_t = 0.0;
+  for (int cw : {8, 4, 2}) {
+    if (!skinny_has(cw, mf)) continue;
+    for (int s : {1, 2, 3, 4, 6, 8}) {
+      if (s > Kc) break;
+      const int kper = (Kc + s - 1) / s;
+      const int splits = (Kc + kper - 1) / kper;
+      if (splits != s) continue;
+      const double part_bytes = splits > 1 ? (double)splits * M * N * 4 : 0.0;
+      if (part_bytes > (double)workspace_bytes) continue;
+      if (skinny_lds(cw, mf, kper) > lds_limit) continue;
+      const double wgs = (double)(N / (16 * cw)) * splits;
+      const double rounds = std::ceil(wgs / cus);
+      const int nk_pad = (kper + 2 * kSkinnyBatch - 1) / (2 * kSkinnyBatch) * (2 * kSkinnyBatch);
+      double t = rounds * nk_pad * (0.40 + 0.19 * cw) * (0.4 + 0.6 * mf / 12.0);
+      if (splits > 1) t += 3.0 + 2.0 * part_bytes / 5.0e6;
+      if (best.cw == 0 || t < best_t) {
+        best_t = t;
+        best = SkinnyPlan{cw, mf, splits, kper};
+      }
+    }
+  }
+  return best;
+}
+
+int64_t fp8_skinny_workspace_bytes(int64_t M, int64_t N, int Kc, int cus, int64_t lds_limit) {
+  const SkinnyPlan pl = fp8_skinny_plan(M, N, Kc, cus, INT64_MAX, lds_limit);
+  return pl.cw > 0 && pl.splits > 1 ? (int64_t)pl.splits * M * N * 4 : 0;
+}
+
+hipError_t launch_fp8_skinny_gemm(const Fp8GemmParams& p, const SkinnyPlan& plan, bool f16_out, float* part,
+                                  hipStream_t stream) {
+  if (p.M == 0) return hipSuccess;
+  if (plan.cw == 0 || !skinny_has(plan.cw, plan.mf) || p.M > 16 * plan.mf || p.N % (16 * plan.cw) != 0 || plan.splits < 1 ||
+      (plan.splits > 1 && part == nullptr) || (int64_t)(plan.splits - 1) * plan.kper >= p.Kc ||
+      (int64_t)plan.splits * plan.kper < p.Kc)
+    return hipErrorInvalidValue;
+  switch (plan.cw) {
+    case 8: return launch_skinny_cw<8>(p, plan.mf, plan.splits, plan.kper, f16_out, part, stream);
+    case 4: return launch_skinny_cw<4>(p, plan.mf, plan.splits, plan.kper, f16_out, part, stream);
+    case 2: return launch_skinny_cw<2>(p, plan.mf, plan.splits, plan.kper, f16_out, part, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
 
 hipError_t launch_fp8_act_quant(const void* x, int64_t x_stride, bool f16_in, void* xq, void* x_scale, int64_t M,
                                 int64_t K, hipStream_t stream) {

@@ -158,6 +158,17 @@ hipError_t launch_fp8_act_quant(const void* x, int64_t x_stride, bool f16_in, vo
 int fp8_gemm_pick_config(int64_t M, int64_t N, int Kc, int cus, int64_t lds_limit);
 int64_t fp8_gemm_lds_bytes(int config, int Kc);
 hipError_t launch_fp8_block_gemm(const Fp8GemmParams& p, int config, bool f16_out, hipStream_t stream);
+// Small-M GEMM (M <= kSkinnyMaxM): cw compute waves of 16 features, mf
+// 16-token fragments, K split into `splits` ranges of kper blocks (cw == 0:
+// no plan; splits > 1 needs splits * M * N fp32 partials).
+constexpr int64_t kSkinnyMaxM = 256;
+struct SkinnyPlan {
+  int cw = 0, mf = 0, splits = 1, kper = 0;
+};
+SkinnyPlan fp8_skinny_plan(int64_t M, int64_t N, int Kc, int cus, int64_t workspace_bytes, int64_t lds_limit);
+int64_t fp8_skinny_workspace_bytes(int64_t M, int64_t N, int Kc, int cus, int64_t lds_limit);
+hipError_t launch_fp8_skinny_gemm(const Fp8GemmParams& p, const SkinnyPlan& plan, bool f16_out, float* part,
+                                  hipStream_t stream);
 
 hipError_t launch_kv_store(const void* key, int64_t key_stride, const void* value,
                            int64_t value_stride, void* k_cache, void* v_cache,

@@ -208,8 +208,12 @@ at::Tensor fp8_block_linear(const at::Tensor& x_in, const at::Tensor& w_in, cons
   check_status(nvamd_fp8_act_quant(x.data_ptr(), x.stride(0), dt, xq.data_ptr(), x_scale.data_ptr(), M, K, stream),
                "fp8_act_quant");
   at::Tensor out = at::empty({M, N}, x.options());
+  const int64_t ws_n = nvamd_fp8_block_gemm_workspace_bytes(M, N, K);
+  at::Tensor ws;
+  if (ws_n > 0) ws = at::empty({ws_n}, x.options().dtype(at::kByte));
   check_status(nvamd_fp8_block_gemm(xq.data_ptr(), x_scale.data_ptr(), w.data_ptr(), w.stride(0), wsc.data_ptr(),
-                                    out.data_ptr(), out.stride(0), dt, M, N, K, stream),
+                                    out.data_ptr(), out.stride(0), dt, M, N, K, ptr_or_null(ws),
+                                    ws.defined() ? ws_n : 0, stream),
                "fp8_block_gemm");
   return out;
 }

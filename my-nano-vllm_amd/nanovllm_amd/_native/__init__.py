@@ -20,7 +20,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 # the torch operators over the C ABI (csrc/torch_ops.cpp), linked against LIB_NAME
 OPS_LIB_NAME = "libnvamd_torch_ops.so"
 OPS_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), OPS_LIB_NAME)
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _c_void_p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -53,7 +53,8 @@ SIGNATURES = {
                             ctypes.c_uint64, _c_void_p, _c_void_p, _i64, _c_void_p]),
     "nvamd_fp8_act_quant": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _i64, _i64, _c_void_p]),
     "nvamd_fp8_block_gemm": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i32,
-                                    _i64, _i64, _i64, _c_void_p]),
+                                    _i64, _i64, _i64, _c_void_p, _i64, _c_void_p]),
+    "nvamd_fp8_block_gemm_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "nvamd_prefill_workspace_bytes": (_i64, [_i64, _i32, _i32, _i32, _i64, _i32, _i32, _i32]),
     "nvamd_fp8_prefill_attention": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                            _c_void_p, _c_void_p, _i64, _i32, _i32, _i32, _i32,

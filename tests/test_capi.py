@@ -88,6 +88,10 @@ def test_fp8_linear_rejects_bad_shapes_without_gpu():
     assert lib.nvamd_fp8_act_quant(None, 128, 2, None, None, 4, 128, None) == 2
     assert lib.nvamd_fp8_act_quant(None, 128, 0, None, None, 4, 128, None) == 1
     assert b"null pointer" in lib.nvamd_last_error()
-    assert lib.nvamd_fp8_block_gemm(None, None, None, 256, None, None, 200, 0, 4, 200, 256, None) == 1
-    assert lib.nvamd_fp8_block_gemm(None, None, None, 256, None, None, 256, 3, 4, 256, 256, None) == 2
-    assert lib.nvamd_fp8_block_gemm(None, None, None, 256, None, None, 256, 0, 0, 256, 256, None) == 0
+    assert lib.nvamd_fp8_block_gemm(None, None, None, 256, None, None, 200, 0, 4, 200, 256, None, 0, None) == 1
+    assert lib.nvamd_fp8_block_gemm(None, None, None, 256, None, None, 256, 3, 4, 256, 256, None, 0, None) == 2
+    assert lib.nvamd_fp8_block_gemm(None, None, None, 256, None, None, 256, 0, 0, 256, 256, None, 0, None) == 0
+    assert lib.nvamd_fp8_block_gemm(None, None, None, 256, None, None, 256, 0, 4, 256, 256, None, 64, None) == 1
+    assert b"null workspace" in lib.nvamd_last_error()
+    assert lib.nvamd_fp8_block_gemm_workspace_bytes(0, 256, 256) == 0
+    assert lib.nvamd_fp8_block_gemm_workspace_bytes(4, 200, 256) == 0

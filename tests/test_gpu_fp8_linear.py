@@ -16,7 +16,11 @@ missing K block errs by about 2^-3.5 of it.
 
 Shapes are chosen so that on a 256-CU MI355X the library picks each of its
 tile shapes (256x256, 128x64, 128x32, 64x16 features x tokens): it takes the
-largest tile whose grid still covers the CUs.
+largest tile whose grid still covers the CUs.  Products with at most 256
+tokens take the small-M kernel instead (weights streamed once; K split over
+workgroups with fp32 partials added in split order when the workspace allows):
+its cases cover 1 to 256 tokens, 2, 4 and 8 compute waves, splits and no
+workspace.
 """
 import numpy as np
 import pytest
@@ -48,8 +52,10 @@ def _scales(g, shape, lo=-4, hi=1):
 ABS_TOL = 2.0 ** -11
 
 
-def _gemm_gpu(xq, x_scale, w, w_scale, out_dtype=torch.bfloat16, w_stride=None, out_stride=None):
-    """Calls nvamd_fp8_block_gemm on device copies; optional padded row strides."""
+def _gemm_gpu(xq, x_scale, w, w_scale, out_dtype=torch.bfloat16, w_stride=None, out_stride=None, ws_bytes=None):
+    """Calls nvamd_fp8_block_gemm on device copies; optional padded row
+    strides; ws_bytes: the workspace given (default: the size the library
+    asks for)."""
     M, K = xq.shape
     N = w.shape[0]
     lib = _native.load()
@@ -62,8 +68,12 @@ def _gemm_gpu(xq, x_scale, w, w_scale, out_dtype=torch.bfloat16, w_stride=None, 
     out_buf = torch.full((max(M, 1), os_), float("nan"), dtype=out_dtype, device="cuda")
     wsc = w_scale.cuda().contiguous()
     code = 0 if out_dtype == torch.bfloat16 else 1
+    if ws_bytes is None:
+        ws_bytes = lib.nvamd_fp8_block_gemm_workspace_bytes(M, N, K)
+    gws = torch.full((max(ws_bytes, 16),), 0x7F, dtype=torch.uint8, device="cuda")  # NaN-filled partials
     st = lib.nvamd_fp8_block_gemm(xq_d.data_ptr(), xs_d.data_ptr(), w_buf.data_ptr(), ws, wsc.data_ptr(),
-                                  out_buf.data_ptr(), os_, code, M, N, K, torch.cuda.current_stream().cuda_stream)
+                                  out_buf.data_ptr(), os_, code, M, N, K, gws.data_ptr() if ws_bytes else None,
+                                  ws_bytes, torch.cuda.current_stream().cuda_stream)
     _native.check(st, "fp8_block_gemm")
     torch.cuda.synchronize()
     if out_stride:
@@ -134,12 +144,16 @@ def test_act_quant_unit_scale_all_patterns_and_strided_rows():
 
 # (M, N, K): tile chosen on 256 CUs -> 256x256: (4096, 4096, 256), and (4096, 4096, 640) with an odd
 # number of K blocks (a token row's scale then sits in either half of its x_scale dword);
-# 128x64: (1024, 2048, 256); 128x32: (1024, 1024, 128); 64x16: the small shapes
-TILE_SHAPES = [(4096, 4096, 256), (4096, 4096, 640), (1024, 2048, 256), (1024, 1024, 128), (24, 256, 512),
-               (1, 128, 128)]
+# 128x64: (1024, 2048, 256); 128x32: (1024, 1024, 128); 64x16: (300, 128, 256)
+TILE_SHAPES = [(4096, 4096, 256), (4096, 4096, 640), (1024, 2048, 256), (1024, 1024, 128), (300, 128, 256)]
+# at most 256 tokens: the Qwen3-8B qkv and down products at 192 tokens take the small-M kernel (down with K
+# split over workgroups), gate/up the 128x64 tile (its grid covers the CUs); 256 tokens (16 token fragments),
+# one token (K split), ragged token counts and odd K block counts on the small-M kernel
+SKINNY_SHAPES = [(192, 6144, 4096), (192, 24576, 4096), (192, 4096, 12288), (256, 1024, 4096), (1, 4096, 4096),
+                 (24, 256, 512), (1, 128, 128), (77, 2048, 1664), (130, 512, 3200)]
 
 
-@pytest.mark.parametrize("M,N,K", TILE_SHAPES)
+@pytest.mark.parametrize("M,N,K", TILE_SHAPES + SKINNY_SHAPES)
 def test_gemm_exact_integer_case(M, N, K):
     """Small-integer codes, power-of-two scales: every fp32 step is exact, so
     the GPU must equal the oracle bit for bit (a transposed operand, a wrong
@@ -238,3 +252,47 @@ def test_fp8_block_linear_matches_oracle(dtype):
     acc = torch.from_numpy(acc).double()
     ulp = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10
     assert not ((got.cpu().double() - acc).abs() > ulp * acc.abs() + ABS_TOL * absum).any()
+
+
+def test_skinny_gemm_split_repeatable_and_without_workspace():
+    """The Qwen3-8B down projection at 192 tokens (K = 12,288 split over
+    workgroups): random codes and scales against the oracle, the same bits on
+    a second call (partials added in split order), and the unsplit product
+    (no workspace) within the same tolerance."""
+    announce("fp8 linear: small-M GEMM 192 x 4096 x 12288, split and unsplit")
+    lib = _native.load()
+    g = torch.Generator().manual_seed(192)
+    M, N, K = 192, 4096, 12288
+    assert lib.nvamd_fp8_block_gemm_workspace_bytes(M, N, K) > 0, "this product splits K"
+    xq, w = _codes(g, (M, K)), _codes(g, (N, K))
+    x_scale, w_scale = _scales(g, (M, K // 128)), _scales(g, (N // 128, K // 128))
+    got = _gemm_gpu(xq, x_scale, w, w_scale)
+    again = _gemm_gpu(xq, x_scale, w, w_scale)
+    assert torch.equal(got.view(torch.int16), again.view(torch.int16)), "split sums differ between calls"
+    unsplit = _gemm_gpu(xq, x_scale, w, w_scale, ws_bytes=0)
+    _, acc = ol.block_gemm(xq.numpy(), _bits(x_scale), w.numpy(), _bits(w_scale))
+    _, absum = _f64(xq, x_scale, w, w_scale)
+    acc = torch.from_numpy(acc).double()
+    for name, out in (("split", got), ("unsplit", unsplit)):
+        bad = (out.double() - acc).abs() > 2.0 ** -7 * acc.abs() + ABS_TOL * absum
+        assert not bad.any(), f"{name}: {int(bad.sum())} outputs off, first at {bad.nonzero()[0].tolist()}"
+
+
+@pytest.mark.parametrize("M,N,K,out_dtype", [(192, 6144, 4096, torch.bfloat16), (256, 2048, 4096, torch.float16),
+                                             (33, 1024, 2048, torch.bfloat16)])
+def test_skinny_gemm_matches_oracle(M, N, K, out_dtype):
+    """Random codes and scales over five decades (two for fp16 outputs) on the
+    small-M kernel, against the oracle's accumulator."""
+    announce(f"fp8 linear: small-M GEMM M={M} N={N} K={K} {out_dtype}")
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    xq, w = _codes(g, (M, K)), _codes(g, (N, K))
+    lo, hi = (-4, 1) if out_dtype == torch.bfloat16 else (-4, -2)
+    x_scale, w_scale = _scales(g, (M, K // 128), lo, hi), _scales(g, (N // 128, K // 128), lo, hi)
+    got = _gemm_gpu(xq, x_scale, w, w_scale, out_dtype).double()
+    _, acc = ol.block_gemm(xq.numpy(), _bits(x_scale), w.numpy(), _bits(w_scale),
+                           "bf16" if out_dtype == torch.bfloat16 else "fp16")
+    _, absum = _f64(xq, x_scale, w, w_scale)
+    acc = torch.from_numpy(acc).double()
+    ulp = 2.0 ** -7 if out_dtype == torch.bfloat16 else 2.0 ** -10
+    bad = (got - acc).abs() > ulp * acc.abs() + ABS_TOL * absum
+    assert not bad.any(), f"{int(bad.sum())} outputs off, first at {bad.nonzero()[0].tolist()}"
