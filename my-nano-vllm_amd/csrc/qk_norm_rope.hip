@@ -23,7 +23,7 @@
 //             out[i + 64] = bf16(z[i + 64] cos_i + z[i] sin_i), i < 64, fp32 math,
 //             cos/sin from the fp32 cos_sin_cache row of the token's position;
 //             lane j (< 8) and lane j + 8 hold the two halves and swap them
-//             with one cross-lane exchange;
+//             with one DPP row rotation;
 //   store:    k (after RoPE) and v (as projected) rounded to E4M3FN (RNE,
 //             satfinite), written to slot_mapping[token] unless it is -1.
 // The sum of squares is reduced in a different order from the reference
@@ -57,9 +57,28 @@ __device__ __forceinline__ u32x2 to_fp8x8(const float (&v)[8]) {
   return u32x2{f32x4_to_fp8x4(v[0], v[1], v[2], v[3]), f32x4_to_fp8x4(v[4], v[5], v[6], v[7])};
 }
 
-__device__ __forceinline__ u32x4 shfl_xor_u32x4(u32x4 w, int mask) {
-  return u32x4{(uint32_t)__shfl_xor((int)w.x, mask, 64), (uint32_t)__shfl_xor((int)w.y, mask, 64),
-               (uint32_t)__shfl_xor((int)w.z, mask, 64), (uint32_t)__shfl_xor((int)w.w, mask, 64)};
+// Cross-lane moves inside a 16-lane DPP row (one head row): rotations by 8
+// and 4 and swaps within quads, all VALU (no LDS round trip).
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, false);
+}
+constexpr int kDppRor8 = 0x128, kDppRor4 = 0x124, kDppXor2 = 0x4E, kDppXor1 = 0xB1;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) { return __builtin_bit_cast(float, dpp_u32<CTRL>(__builtin_bit_cast(uint32_t, v))); }
+
+// sum over the 16 lanes of the row, in every lane
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp_f32<kDppRor8>(x);   // lanes i, i + 8
+  x += dpp_f32<kDppRor4>(x);   // + i + 4, i + 12
+  x += dpp_f32<kDppXor2>(x);   // + the other pair of the quad
+  return x + dpp_f32<kDppXor1>(x);
+}
+
+// lane j of the row <- lane j ^ 8 (the other half of the head dims)
+__device__ __forceinline__ u32x4 swap_halves(u32x4 w) {
+  return u32x4{dpp_u32<kDppRor8>(w.x), dpp_u32<kDppRor8>(w.y), dpp_u32<kDppRor8>(w.z), dpp_u32<kDppRor8>(w.w)};
 }
 
 }  // namespace
@@ -72,6 +91,8 @@ __device__ __forceinline__ u32x4 shfl_xor_u32x4(u32x4 w, int mask) {
 constexpr int kRowsPerPass = 256 / kLanesPerRow;  // 16 head rows per pass of the workgroup
 constexpr int kMaxPasses = 8;                      // rows of a token: at most 128 (checked at launch)
 
+// NP passes: ceil((Hq + 2 Hkv) / 16) (3 for Qwen3-8B's 32 + 2 x 8 rows)
+template <int NP>
 __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(QkNormRopeParams p) {
   const int rows_per_token = p.Hq + 2 * p.Hkv;
   const int64_t tok = blockIdx.x;
@@ -87,9 +108,9 @@ __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(QkNormRopeParam
   const uint16_t* xrow = p.qkv + tok * p.qkv_stride + 8 * j;
 
   // this lane's rows: all loads first
-  u32x4 xr[kMaxPasses];
+  u32x4 xr[NP];
 #pragma unroll
-  for (int i = 0; i < kMaxPasses; ++i) {
+  for (int i = 0; i < NP; ++i) {
     const int r = g + kRowsPerPass * i;
     xr[i] = r < rows_per_token ? *reinterpret_cast<const u32x4*>(xrow + (int64_t)r * kHeadDim) : u32x4{0u, 0u, 0u, 0u};
   }
@@ -106,7 +127,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(QkNormRopeParam
   const float sgn = (j < 8) ? -1.f : 1.f;  // first half: z cos - other sin; second: z cos + other sin
 
 #pragma unroll
-  for (int i = 0; i < kMaxPasses; ++i) {
+  for (int i = 0; i < NP; ++i) {
     const int r = g + kRowsPerPass * i;  // uniform in a 16-lane group, so the exchanges below stay in live lanes
     if (r >= rows_per_token) break;
     float x[8];
@@ -120,8 +141,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(QkNormRopeParam
     float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(x[e], x[e], ss);
-#pragma unroll
-    for (int m = 1; m < kLanesPerRow; m <<= 1) ss += shfl_xor_f32(ss, m);
+    ss = row16_sum(ss);
     const float rs = __builtin_amdgcn_rsqf(ss * (1.0f / kHeadDim) + p.eps);
     float z[8];
 #pragma unroll
@@ -132,7 +152,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(QkNormRopeParam
     // RoPE
     const u32x4 zp = pack8_bf16(z);  // exact: z is bf16
     float other[8];
-    unpack8_bf16(shfl_xor_u32x4(zp, 8), other);
+    unpack8_bf16(swap_halves(zp), other);
     float o[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e)
@@ -151,7 +171,17 @@ __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(QkNormRopeParam
 hipError_t launch_qk_norm_rope_store(const QkNormRopeParams& p, hipStream_t stream) {
   if (p.num_tokens == 0) return hipSuccess;
   if (p.num_tokens > 0x7fffffff || p.Hq + 2 * p.Hkv > kRowsPerPass * kMaxPasses) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(qk_norm_rope_store_kernel, dim3((unsigned)p.num_tokens), dim3(256), 0, stream, p);
+  const dim3 grid((unsigned)p.num_tokens), block(256);
+  switch ((p.Hq + 2 * p.Hkv + kRowsPerPass - 1) / kRowsPerPass) {
+    case 1: hipLaunchKernelGGL(qk_norm_rope_store_kernel<1>, grid, block, 0, stream, p); break;
+    case 2: hipLaunchKernelGGL(qk_norm_rope_store_kernel<2>, grid, block, 0, stream, p); break;
+    case 3: hipLaunchKernelGGL(qk_norm_rope_store_kernel<3>, grid, block, 0, stream, p); break;
+    case 4: hipLaunchKernelGGL(qk_norm_rope_store_kernel<4>, grid, block, 0, stream, p); break;
+    case 5: hipLaunchKernelGGL(qk_norm_rope_store_kernel<5>, grid, block, 0, stream, p); break;
+    case 6: hipLaunchKernelGGL(qk_norm_rope_store_kernel<6>, grid, block, 0, stream, p); break;
+    case 7: hipLaunchKernelGGL(qk_norm_rope_store_kernel<7>, grid, block, 0, stream, p); break;
+    default: hipLaunchKernelGGL(qk_norm_rope_store_kernel<8>, grid, block, 0, stream, p); break;
+  }
   return hipGetLastError();
 }
 

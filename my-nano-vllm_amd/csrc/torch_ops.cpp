@@ -18,6 +18,7 @@
 // FakeTensor / torch.compile tracing the output shapes.
 #include <ATen/ATen.h>
 #include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPCachingAllocator.h>
 #include <c10/hip/HIPStream.h>
 #include <torch/library.h>
 
@@ -55,12 +56,13 @@ void check_status(int32_t st, const char* what) {
   TORCH_CHECK(st == NVAMD_OK, what, " failed (status ", st, "): ", nvamd_last_error());
 }
 
-at::Tensor workspace(int64_t nbytes, const at::Tensor& like) {
-  if (nbytes <= 0) return at::Tensor();
-  return at::empty({nbytes}, like.options().dtype(at::kByte));
+// Scratch straight from torch's caching allocator on the current device (no
+// tensor, no dispatcher call); freed when the call returns, which the
+// allocator orders after the work already enqueued on the stream.
+c10::DataPtr workspace(int64_t nbytes) {
+  if (nbytes <= 0) return c10::DataPtr();
+  return c10::hip::HIPCachingAllocator::get()->allocate((size_t)nbytes);
 }
-
-void* ptr_or_null(const at::Tensor& t) { return t.defined() ? t.data_ptr() : nullptr; }
 
 // attention.py:33-40, with the reference's assertions.
 void store_kvcache(const at::Tensor& key, const at::Tensor& value, const at::Tensor& k_cache,
@@ -114,12 +116,12 @@ at::Tensor decode(const at::Tensor& q_in, const at::Tensor& k_in, const at::Tens
   const at::OptionalDeviceGuard guard(q.device());
   const int64_t ws_n = nvamd_decode_workspace_bytes((int32_t)batch, (int32_t)num_heads, (int32_t)num_kv_heads,
                                                     (int32_t)max_num_blocks, (int32_t)block_size, 0);
-  const at::Tensor ws = workspace(ws_n, q);
+  const c10::DataPtr ws = workspace(ws_n);
   check_status(nvamd_fp8_decode_attention(out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
                                           bt.data_ptr<int32_t>(), ctx.data_ptr<int32_t>(), (int32_t)batch,
                                           (int32_t)num_heads, (int32_t)num_kv_heads, (int32_t)head_dim, num_blocks,
                                           (int32_t)block_size, (int32_t)max_num_blocks, (float)softmax_scale, 0,
-                                          ptr_or_null(ws), ws.defined() ? ws_n : 0, dt, stream_of(q)),
+                                          ws.get(), ws.get() != nullptr ? ws_n : 0, dt, stream_of(q)),
                "fp8_decode_attention");
   return out;
 }
@@ -166,14 +168,14 @@ at::Tensor prefill(const at::Tensor& q_in, const at::Tensor& k_in, const at::Ten
   const int64_t ws_n = nvamd_prefill_workspace_bytes(num_tokens, (int32_t)num_seqs, (int32_t)num_heads,
                                                      (int32_t)num_kv_heads, kv_cap, (int32_t)max_seqlen_q,
                                                      (int32_t)block_size, 0);
-  const at::Tensor ws = workspace(ws_n, q);
+  const c10::DataPtr ws = workspace(ws_n);
   check_status(nvamd_fp8_prefill_attention(out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
                                            paged ? bt.data_ptr<int32_t>() : nullptr, cu_q.data_ptr<int32_t>(),
                                            cu_k.data_ptr<int32_t>(), num_tokens, (int32_t)num_seqs,
                                            (int32_t)num_heads, (int32_t)num_kv_heads, (int32_t)head_dim,
                                            num_kv_rows, (int32_t)block_size, (int32_t)max_num_blocks,
                                            (int32_t)max_seqlen_q, (int32_t)max_seqlen_k, (float)softmax_scale, 0,
-                                           ptr_or_null(ws), ws.defined() ? ws_n : 0, dt, stream_of(q)),
+                                           ws.get(), ws.get() != nullptr ? ws_n : 0, dt, stream_of(q)),
                "fp8_prefill_attention");
   return out;
 }
@@ -203,17 +205,17 @@ at::Tensor fp8_block_linear(const at::Tensor& x_in, const at::Tensor& w_in, cons
   const at::Tensor wsc = (ws_in.scalar_type() == at::kBFloat16 ? ws_in : ws_in.to(at::kBFloat16)).contiguous();
   const at::OptionalDeviceGuard guard(x.device());
   const hipStream_t stream = stream_of(x);
-  at::Tensor xq = at::empty({M, K}, x.options().dtype(at::kFloat8_e4m3fn));
-  at::Tensor x_scale = at::empty({M, K / 128}, x.options().dtype(at::kBFloat16));
-  check_status(nvamd_fp8_act_quant(x.data_ptr(), x.stride(0), dt, xq.data_ptr(), x_scale.data_ptr(), M, K, stream),
-               "fp8_act_quant");
+  // the quantised activations [M, K] and their bf16 scales [M, K/128], one allocation
+  const int64_t xq_bytes = (M * K + 255) / 256 * 256;
+  const c10::DataPtr act = workspace(xq_bytes + M * (K / 128) * 2);
+  void* xq = act.get();
+  void* x_scale = static_cast<char*>(act.get()) + xq_bytes;
+  check_status(nvamd_fp8_act_quant(x.data_ptr(), x.stride(0), dt, xq, x_scale, M, K, stream), "fp8_act_quant");
   at::Tensor out = at::empty({M, N}, x.options());
   const int64_t ws_n = nvamd_fp8_block_gemm_workspace_bytes(M, N, K);
-  at::Tensor ws;
-  if (ws_n > 0) ws = at::empty({ws_n}, x.options().dtype(at::kByte));
-  check_status(nvamd_fp8_block_gemm(xq.data_ptr(), x_scale.data_ptr(), w.data_ptr(), w.stride(0), wsc.data_ptr(),
-                                    out.data_ptr(), out.stride(0), dt, M, N, K, ptr_or_null(ws),
-                                    ws.defined() ? ws_n : 0, stream),
+  const c10::DataPtr ws = workspace(ws_n);
+  check_status(nvamd_fp8_block_gemm(xq, x_scale, w.data_ptr(), w.stride(0), wsc.data_ptr(), out.data_ptr(),
+                                    out.stride(0), dt, M, N, K, ws.get(), ws.get() != nullptr ? ws_n : 0, stream),
                "fp8_block_gemm");
   return out;
 }
