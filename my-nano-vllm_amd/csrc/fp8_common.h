@@ -185,6 +185,33 @@ __device__ __forceinline__ float shfl_xor_f32(float v, int mask) {
   return __shfl_xor(v, mask, 64);
 }
 
+// Cross-lane moves inside a 16-lane DPP row: rotations by 8 and 4 and
+// swaps within quads, all VALU (no LDS round trip as with __shfl_xor).
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, false);
+}
+constexpr int kDppRor8 = 0x128, kDppRor4 = 0x124, kDppXor2 = 0x4E, kDppXor1 = 0xB1;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(float, dpp_u32<CTRL>(__builtin_bit_cast(uint32_t, v)));
+}
+
+// sum / maximum over the 16 lanes of a row, in every lane
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp_f32<kDppRor8>(x);  // lanes i, i + 8
+  x += dpp_f32<kDppRor4>(x);  // + i + 4, i + 12
+  x += dpp_f32<kDppXor2>(x);  // + the other pair of the quad
+  return x + dpp_f32<kDppXor1>(x);
+}
+__device__ __forceinline__ float row16_max(float x) {
+  x = fmaxf(x, dpp_f32<kDppRor8>(x));
+  x = fmaxf(x, dpp_f32<kDppRor4>(x));
+  x = fmaxf(x, dpp_f32<kDppXor2>(x));
+  return fmaxf(x, dpp_f32<kDppXor1>(x));
+}
+
 // Inclusive prefix sum over the 64 lanes of a wave: inside each row of 16
 // lanes by DPP row shifts (a lane whose source is before its row's start
 // adds 0), then the totals of the rows before it (lanes 15, 31, 47) through

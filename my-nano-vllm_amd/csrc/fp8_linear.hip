@@ -8,7 +8,7 @@
 // Quantisation: one 16-lane group per (token m, 128-column group g), the
 // token from the workgroup's index; lane j loads 8 consecutive values (one
 // 16-byte load).  amax over the group by
-// cross-lane exchange; scale = amax / 448 (IEEE fp32 division), 1 when not
+// DPP row exchanges; scale = amax / 448 (IEEE fp32 division), 1 when not
 // > 0; xq = E4M3FN(clamp(x / scale)) (IEEE division, RNE); the scale is stored
 // as bf16 (RNE), x_scale[m, g].  Purely HBM-bound: 2 B read + 1 B written per
 // element.
@@ -81,8 +81,7 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restri
   float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) amax = fmaxf(amax, __builtin_fabsf(v[i]));
-#pragma unroll
-  for (int s = 1; s < 16; s <<= 1) amax = fmaxf(amax, shfl_xor_f32(amax, s));
+  amax = row16_max(amax);  // the group's 16 lanes are one DPP row
   float scale = amax / 448.0f;  // correctly rounded fp32 division
   scale = scale > 0.f ? scale : 1.0f;
   float y[8];

@@ -57,25 +57,6 @@ __device__ __forceinline__ u32x2 to_fp8x8(const float (&v)[8]) {
   return u32x2{f32x4_to_fp8x4(v[0], v[1], v[2], v[3]), f32x4_to_fp8x4(v[4], v[5], v[6], v[7])};
 }
 
-// Cross-lane moves inside a 16-lane DPP row (one head row): rotations by 8
-// and 4 and swaps within quads, all VALU (no LDS round trip).
-template <int CTRL>
-__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, false);
-}
-constexpr int kDppRor8 = 0x128, kDppRor4 = 0x124, kDppXor2 = 0x4E, kDppXor1 = 0xB1;
-
-template <int CTRL>
-__device__ __forceinline__ float dpp_f32(float v) { return __builtin_bit_cast(float, dpp_u32<CTRL>(__builtin_bit_cast(uint32_t, v))); }
-
-// sum over the 16 lanes of the row, in every lane
-__device__ __forceinline__ float row16_sum(float x) {
-  x += dpp_f32<kDppRor8>(x);   // lanes i, i + 8
-  x += dpp_f32<kDppRor4>(x);   // + i + 4, i + 12
-  x += dpp_f32<kDppXor2>(x);   // + the other pair of the quad
-  return x + dpp_f32<kDppXor1>(x);
-}
-
 // lane j of the row <- lane j ^ 8 (the other half of the head dims)
 __device__ __forceinline__ u32x4 swap_halves(u32x4 w) {
   return u32x4{dpp_u32<kDppRor8>(w.x), dpp_u32<kDppRor8>(w.y), dpp_u32<kDppRor8>(w.z), dpp_u32<kDppRor8>(w.w)};

@@ -18,6 +18,15 @@ attention call of nano-vLLM's Qwen3 layer:
 
 ``rope_cache`` builds the reference's cos/sin table (rotary_embedding.py:26-33).
 
+The reference's RMSNorm and RoPE run under ``@torch.compile``
+(layernorm.py:16, rotary_embedding.py:37).  Its source rounds the
+normalised row to bf16 before the weight product (``x.to(orig_dtype).mul_
+(self.weight)``), which eager mode executes as written; inductor, with its
+default ``emulate_precision_casts = False``, may fuse the downcast and the
+following upcast away and round once, after the product.  ``fused_norm``
+selects that single-rounding form (RoPE has no intermediate rounding in
+either mode: fp32 math, one cast at the end).
+
 Pinned by tests/test_oracle_qk_norm_rope.py: RMSNorm against torch's own
 ``rms_norm`` in float64 and the constant-vector closed form; RoPE against a
 complex multiplication in float64, position 0 as the identity and the
@@ -36,12 +45,15 @@ def rope_cache(head_dim, max_position, base):
     return torch.cat((angles.cos(), angles.sin()), dim=-1)
 
 
-def rms_norm_bf16(x, weight, eps):
-    """x: bf16 [..., D]; weight: bf16 [D] -> bf16 [..., D] (layernorm.py:16-25)."""
+def rms_norm_bf16(x, weight, eps, fused_norm=False):
+    """x: bf16 [..., D]; weight: bf16 [D] -> bf16 [..., D] (layernorm.py:16-25);
+    fused_norm: one rounding after the weight product instead of two."""
     xf = x.float()
     var = xf.pow(2).mean(dim=-1, keepdim=True)
-    y = (xf * torch.rsqrt(var + eps)).to(torch.bfloat16)
-    return (y.float() * weight.float()).to(torch.bfloat16)
+    y = xf * torch.rsqrt(var + eps)
+    if not fused_norm:
+        y = y.to(torch.bfloat16).float()
+    return (y * weight.float()).to(torch.bfloat16)
 
 
 def rope_bf16(x, positions, cache):
@@ -55,7 +67,7 @@ def rope_bf16(x, positions, cache):
 
 
 def qk_norm_rope_store(qkv, num_heads, num_kv_heads, head_dim, positions, q_weight, k_weight, eps, cache,
-                       k_cache, v_cache, slot_mapping):
+                       k_cache, v_cache, slot_mapping, fused_norm=False):
     """qkv: bf16 [N, (Hq + 2 Hkv) * D]; k_cache/v_cache: uint8 [P, bs, Hkv, D]
     written in place (rows with slot -1 skipped).  Returns (q, k): bf16
     [N, Hq, D] and [N, Hkv, D] after RMSNorm and RoPE."""
@@ -64,7 +76,7 @@ def qk_norm_rope_store(qkv, num_heads, num_kv_heads, head_dim, positions, q_weig
     q = qkv[:, :q_size].reshape(n, num_heads, head_dim)
     k = qkv[:, q_size:q_size + kv_size].reshape(n, num_kv_heads, head_dim)
     v = qkv[:, q_size + kv_size:q_size + 2 * kv_size].reshape(n, num_kv_heads, head_dim)
-    q = rope_bf16(rms_norm_bf16(q, q_weight, eps), positions, cache)
-    k = rope_bf16(rms_norm_bf16(k, k_weight, eps), positions, cache)
+    q = rope_bf16(rms_norm_bf16(q, q_weight, eps, fused_norm), positions, cache)
+    k = rope_bf16(rms_norm_bf16(k, k_weight, eps, fused_norm), positions, cache)
     _fp8.store_kvcache(k, v, k_cache, v_cache, slot_mapping)
     return q, k

@@ -30,6 +30,24 @@ def test_rms_norm_matches_float64_rms_norm_then_weight():
     assert (got == want).float().mean() > 0.995  # fp32 vs fp64 only flips rare rounding boundaries
 
 
+def test_fused_rms_norm_rounds_once():
+    """The single-rounding form (inductor without emulated precision casts):
+    within half a bf16 ulp of the float64 product rms_norm(x) * w (one
+    rounding of a value computed in fp32), and the two-rounding form differs
+    from it by at most one ulp, in a minority of elements."""
+    x = _bf16(64, 8, D, seed=11, scale=3.0)
+    w = (1.0 + 0.1 * _bf16(D, seed=12).float()).to(torch.bfloat16)
+    eps = 1e-6
+    fused = oq.rms_norm_bf16(x, w, eps, fused_norm=True)
+    exact = torch.nn.functional.rms_norm(x.double(), (D,), eps=eps) * w.double()
+    ulp = fused.double().abs().clamp(min=1e-30) * 2.0 ** -7
+    assert bool(((fused.double() - exact).abs() <= 0.5 * ulp * 1.01).all())
+    eager = oq.rms_norm_bf16(x, w, eps)
+    assert bool(((eager.double() - fused.double()).abs() <= ulp * 1.01).all())
+    same = (eager == fused).float().mean().item()
+    assert 0.5 < same < 1.0, same  # double rounding moves some elements, not most
+
+
 def test_rms_norm_constant_vector_gives_the_weight():
     w = _bf16(D, seed=3)
     for c in (0.5, -3.0, 100.0):
