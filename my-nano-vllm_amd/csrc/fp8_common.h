@@ -212,6 +212,29 @@ __device__ __forceinline__ float row16_max(float x) {
   return fmaxf(x, dpp_f32<kDppXor1>(x));
 }
 
+// max / sum over the 64 lanes of a wave, in every lane: DPP inside each row,
+// then the gfx950 row swaps (permlane16/32_swap(x, x) leave a lane holding
+// x[l] and x[l ^ 16], resp. x[l ^ 32], in its two results).
+__device__ __forceinline__ float swap16_pair(float x, bool sum) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const float a0 = __builtin_bit_cast(float, (uint32_t)a[0]), a1 = __builtin_bit_cast(float, (uint32_t)a[1]);
+  return sum ? a0 + a1 : fmaxf(a0, a1);
+}
+__device__ __forceinline__ float swap32_pair(float x, bool sum) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const float a0 = __builtin_bit_cast(float, (uint32_t)a[0]), a1 = __builtin_bit_cast(float, (uint32_t)a[1]);
+  return sum ? a0 + a1 : fmaxf(a0, a1);
+}
+__device__ __forceinline__ float wave_max_f32(float x) { return swap32_pair(swap16_pair(row16_max(x), false), false); }
+__device__ __forceinline__ float wave_sum_f32(float x) { return swap32_pair(swap16_pair(row16_sum(x), true), true); }
+
+// lane j's value, in every lane (j wave-uniform)
+__device__ __forceinline__ float readlane_f32(float x, int j) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), j));
+}
+
 // Inclusive prefix sum over the 64 lanes of a wave: inside each row of 16
 // lanes by DPP row shifts (a lane whose source is before its row's start
 // adds 0), then the totals of the rows before it (lanes 15, 31, 47) through

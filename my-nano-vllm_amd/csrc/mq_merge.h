@@ -38,8 +38,7 @@ __device__ __forceinline__ void merge_partitions(const MqParams& p, int64_t rh, 
     const float m = ml[2 * (c + min(lane, qn - 1))];
     M = fmaxf(M, lane < qn ? m : -INFINITY);
   }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, shfl_xor_f32(M, off));
+  M = wave_max_f32(M);  // DPP and row swaps: no LDS round trip
   const float Ms = (M == -INFINITY) ? 0.f : M;
 
   float L = 0.f, o0 = 0.f, o1 = 0.f;
@@ -63,8 +62,7 @@ __device__ __forceinline__ void merge_partitions(const MqParams& p, int64_t rh, 
       }
     }
   }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) L += shfl_xor_f32(L, off);
+  L = wave_sum_f32(L);
   const float inv = (L > 0.f) ? 1.0f / L : 0.f;
   const bool f16 = p.out_f16 != 0;
   const uint32_t w = out_bits_rt(o0 * inv, f16) | (out_bits_rt(o1 * inv, f16) << 16);
@@ -227,10 +225,9 @@ __device__ __forceinline__ void sk_merge_one(const MqParams& p, int b, int idx, 
         }
       }
     }
-    float Mp = mi;
-#pragma unroll
-    for (int off = 4; off > 0; off >>= 1) Mp = fmaxf(Mp, shfl_xor_f32(Mp, off));
-    Mp = __shfl(Mp, 0, 64);  // lanes 0..7 hold the chunk's values
+    // lanes 0..7 hold the chunk's values (the rest -inf and 0): DPP inside
+    // the first row, then lane 0's result read by every lane
+    const float Mp = readlane_f32(row16_max(mi), 0);
     const float Mn = fmaxf(M, Mp);
     const float Ms = (Mn == -INFINITY) ? 0.f : Mn;
     const float sc = (M == -INFINITY) ? 0.f : fast_exp2(M - Ms);
@@ -239,13 +236,11 @@ __device__ __forceinline__ void sk_merge_one(const MqParams& p, int b, int idx, 
     o1 *= sc;
     M = Mn;
     const float wi = (mi == -INFINITY) ? 0.f : fast_exp2(mi - Ms);
-    float lw = li * wi;
-#pragma unroll
-    for (int off = 4; off > 0; off >>= 1) lw += shfl_xor_f32(lw, off);
-    Lsum += __shfl(lw, 0, 64);
+    const float lw = li * wi;
+    Lsum += readlane_f32(row16_sum(lw), 0);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {  // weight of a normalised partial: w_j * l_j
-      const float wk = __shfl(li * wi, j, 64);
+      const float wk = readlane_f32(lw, j);
       const f16x2 h = __builtin_bit_cast(f16x2, a[j]);
       o0 += wk * (float)h.x;
       o1 += wk * (float)h.y;

@@ -465,8 +465,7 @@ __device__ __forceinline__ void mq_attn(const MqParams& p, const int part, const
   float* sm_ml = sm_o + kWaves * 16 * kPitch;                         // [4 waves][NCB*16][2]
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) {
-    lsum[cb] += shfl_xor_f32(lsum[cb], 16);   // once per partition
-    lsum[cb] += shfl_xor_f32(lsum[cb], 32);
+    lsum[cb] = swap32_pair(swap16_pair(lsum[cb], true), true);  // once per partition: + lanes l ^ 16, then l ^ 32
     if (gam == 0) {
       sm_ml[(wave * NCB * 16 + 16 * cb + r) * 2 + 0] = m[cb];
       sm_ml[(wave * NCB * 16 + 16 * cb + r) * 2 + 1] = lsum[cb];
@@ -922,8 +921,7 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p, PrefillP
   auto end_segment = [&](bool full) {
 #pragma unroll
     for (int cb = 0; cb < NCB; ++cb) {
-      lsum[cb] += shfl_xor_f32(lsum[cb], 16);
-      lsum[cb] += shfl_xor_f32(lsum[cb], 32);
+      lsum[cb] = swap32_pair(swap16_pair(lsum[cb], true), true);  // + lanes l ^ 16, then l ^ 32
       const int col = 16 * cb + r;
       if (col_row[cb] < 0) continue;
       if (full) {
