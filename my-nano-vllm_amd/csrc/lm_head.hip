@@ -106,6 +106,43 @@ __device__ __forceinline__ float load1(const void* row, int64_t v) {
   else return static_cast<const float*>(row)[v];
 }
 
+// (value, index): larger value wins, the smaller index on equal values
+__device__ __forceinline__ void better_i32(float& v, int& i, float ov, int oi) {
+  if (ov > v || (ov == v && oi < i)) {
+    v = ov;
+    i = oi;
+  }
+}
+
+// Best (value, index) over the wave, in every lane.  The order is total, so
+// any reduction order gives the same winner: DPP inside each 16-lane row,
+// then the gfx950 row swaps (no LDS round trip).
+template <int CTRL>
+__device__ __forceinline__ void best_dpp(float& v, int& i) {
+  better_i32(v, i, dpp_f32<CTRL>(v), (int)dpp_u32<CTRL>((uint32_t)i));
+}
+__device__ __forceinline__ void best_swap(float& v, int& i, bool swap32) {
+  const uint32_t uv = __builtin_bit_cast(uint32_t, v), ui = (uint32_t)i;
+  const auto a = swap32 ? __builtin_amdgcn_permlane32_swap(uv, uv, false, false)
+                        : __builtin_amdgcn_permlane16_swap(uv, uv, false, false);
+  const auto b = swap32 ? __builtin_amdgcn_permlane32_swap(ui, ui, false, false)
+                        : __builtin_amdgcn_permlane16_swap(ui, ui, false, false);
+  const uint32_t a0 = a[0], a1 = a[1], b0 = b[0], b1 = b[1];
+  float v0 = __builtin_bit_cast(float, a0);
+  int i0 = (int)b0;
+  better_i32(v0, i0, __builtin_bit_cast(float, a1), (int)b1);
+  v = v0;
+  i = i0;
+}
+__device__ __forceinline__ void wave_best(float& v, int& i) {
+  best_dpp<kDppRor8>(v, i);
+  best_dpp<kDppRor4>(v, i);
+  best_dpp<kDppXor2>(v, i);
+  best_dpp<kDppXor1>(v, i);
+  best_swap(v, i, false);
+  best_swap(v, i, true);
+}
+
 // Part `part` of row `row` with the caller's noise: 4-element blocks [j0, j1)
 // (elements 4j .. 4j + 3).  score_v = z_v * log2(e) / T - log2(max(E_v,
 // 1e-10)); the row's argmax of score equals the reference's argmax of
@@ -158,15 +195,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_part_kernel(
       bi = up ? v0 + i : bi;
     }
   }
-  // (value, index): larger value wins, the smaller index on equal values
-  auto better32 = [](float& v, int& i, float ov, int oi) {
-    if (ov > v || (ov == v && oi < i)) {
-      v = ov;
-      i = oi;
-    }
-  };
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) better32(bv, bi, __shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64));
+  wave_best(bv, bi);
   const int w = tid >> 6;
   if ((tid & 63) == 0) {
     bval[w] = bv;
@@ -174,7 +203,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_part_kernel(
   }
   __syncthreads();
   if (tid == 0) {
-    for (int i = 1; i < kSampleThreads / 64; ++i) better32(bv, bi, bval[i], bidx[i]);
+    for (int i = 1; i < kSampleThreads / 64; ++i) better_i32(bv, bi, bval[i], bidx[i]);
     part_score[blockIdx.x] = bv;
     part_index[blockIdx.x] = bi;
   }
@@ -212,19 +241,6 @@ __device__ __forceinline__ void load_group(const void* row, int t0, int vocab, f
 __device__ __forceinline__ float gumbel_log2(uint32_t x) {
   const float e = -__builtin_amdgcn_logf((float)((x >> 8) + 1u) * 0x1p-24f) * 0.6931471805599453f;
   return -__builtin_amdgcn_logf(fmaxf(e, 1e-10f));
-}
-
-// (value, index): larger value wins, the smaller index on equal values
-__device__ __forceinline__ void better_i32(float& v, int& i, float ov, int oi) {
-  if (ov > v || (ov == v && oi < i)) {
-    v = ov;
-    i = oi;
-  }
-}
-
-__device__ __forceinline__ void wave_best(float& v, int& i) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) better_i32(v, i, __shfl_xor(v, o, 64), __shfl_xor(i, o, 64));
 }
 
 // One wave per (row, quad): lane l takes group 64k + l of each of the quad's
