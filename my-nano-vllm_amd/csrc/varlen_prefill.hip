@@ -695,7 +695,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
   else tile_loop(std::false_type{});
 
   // ---- normalise and store ----------------------------------------------------
-  l_run += shfl_xor_f32(l_run, 32);
+  l_run = swap32_pair(l_run, true);  // + lane l ^ 32 (row swap, no LDS round trip)
   if (n_pieces > 1) {
     // A piece of a split item: write this lane's partial (accumulators
     // normalised, fp16; m, l) to the piece's slot; the item's last piece to
