@@ -251,4 +251,96 @@ __device__ __forceinline__ void sk_merge_one(const MqParams& p, int b, int idx, 
   out[lane] = out_bits_rt(o0 * inv, f16) | (out_bits_rt(o1 * inv, f16) << 16);
 }
 
+// Decode (one query row per sequence) with G <= 4 query heads per kv head:
+// the merge of one (sequence, kv head) by one wave, 16 lanes per query head
+// (8 dims each), so a wave covers the kv head's G heads with the same two
+// memory round trips (the pair's prefix, then every contributor's partial) as
+// sk_merge_one takes for one head, and the launch has a quarter of the waves.
+// Every lane loads each contributor's (m, l) itself (the 16 lanes of a head
+// share the address), so no cross-lane exchange is needed; the contributors
+// are added in workgroup order.
+__device__ __forceinline__ void sk_merge_heads(const MqParams& p, int b, int kvh, int lane) {
+  const int G = p.G, HG = p.sk_heads, NHG = p.Hkv / HG;
+  const int sub = lane >> 4, d8 = lane & 15;  // query head kvh * G + sub, dims 8 d8 .. 8 d8 + 7
+  const int hg = kvh / HG, hh = kvh - hg * HG;
+  const int pre_b = p.sk_prefix[b];
+  const int n = p.sk_prefix[b + 1] - pre_b;
+  u32x4* out = reinterpret_cast<u32x4*>(p.out + ((int64_t)b * p.Hq + kvh * G + sub) * kHeadDim + 8 * d8);
+  if (n == 0) {
+    // Empty context (graph padding rows): the reference yields NaN here; write 0.
+    if (sub < G) *out = u32x4{0u, 0u, 0u, 0u};
+    return;
+  }
+  const int W = p.sk_wgs;
+  const int64_t T = (int64_t)NHG * p.sk_prefix[p.num_seqs];
+  const int64_t P = (int64_t)NHG * pre_b + (int64_t)hg * n;
+  const int a = sk_even_weight(p);
+  int wf, wl, slot_f;
+  if (sk_fits32(T, W, a)) sk_pair_owners<uint32_t>((uint32_t)P, (uint32_t)n, (uint32_t)T, (uint32_t)W, (uint32_t)a, wf, wl, slot_f);
+  else sk_pair_owners<uint64_t>((uint64_t)P, (uint64_t)n, (uint64_t)T, (uint64_t)W, (uint64_t)a, wf, wl, slot_f);
+  if (wf == wl) return;  // finished by its workgroup
+  // slot s of workgroup w for (hh, col) at base + (2w + s) * wstride (as in sk_merge_one)
+  const int col = min(sub, G - 1);
+  const float* base = p.sk_part + (int64_t)(hh * p.sk_cols + col) * kSkSlotFloats;
+  const int64_t wstride = (int64_t)HG * p.sk_cols * kSkSlotFloats;
+  const bool may_be_empty = T < W;  // then workgroups with empty ranges wrote nothing
+  float M = -INFINITY, L = 0.f, o[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = 0.f;
+  for (int w0 = wf; w0 <= wl; w0 += 8) {
+    const int cnt = min(8, wl - w0 + 1);
+    uint32_t use = (1u << cnt) - 1u;  // bit j: contributor w0 + j wrote a partial
+    if (may_be_empty) {
+#pragma nounroll
+      for (int j = 0; j < cnt; ++j)
+        if (sk_range_start<uint32_t>(w0 + j, (uint32_t)T, W, a) ==  // T < W: T * C(W) < 2^32
+            sk_range_start<uint32_t>(w0 + j + 1, (uint32_t)T, W, a))
+          use &= ~(1u << j);
+    }
+    u32x4 h[8];
+    f32x2 ml[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {  // all of the chunk's loads before any is used: one round trip
+      // a contributor without a partial reads wl's instead (its weight is zero
+      // and the skipped slot may hold anything, NaN included)
+      const int w = ((use >> j) & 1u) ? w0 + j : wl;
+      const float* ps = base + (int64_t)(2 * w + (w == wf ? slot_f : 0)) * wstride;
+      h[j] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(ps) + 8 * d8);
+      ml[j] = *reinterpret_cast<const f32x2*>(ps + kSkSlotMl);
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mx = ((use >> j) & 1u) ? fmaxf(mx, ml[j].x) : mx;
+    const float Mn = fmaxf(M, mx);
+    const float Ms = (Mn == -INFINITY) ? 0.f : Mn;
+    const float sc = (M == -INFINITY) ? 0.f : fast_exp2(M - Ms);
+    L *= sc;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] *= sc;
+    M = Mn;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {  // weight of a normalised partial: w_j * l_j
+      const bool u = ((use >> j) & 1u) && ml[j].x != -INFINITY;
+      const float wk = u ? fast_exp2(ml[j].x - Ms) * ml[j].y : 0.f;
+      L += wk;
+      const uint32_t hw[4] = {h[j].x, h[j].y, h[j].z, h[j].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const f16x2 h2 = __builtin_bit_cast(f16x2, hw[e]);
+        o[2 * e] += wk * (float)h2.x;
+        o[2 * e + 1] += wk * (float)h2.y;
+      }
+    }
+  }
+  if (sub >= G) return;
+  const float inv = (L > 0.f) ? 1.0f / L : 0.f;
+  const bool f16 = p.out_f16 != 0;
+  u32x4 v;
+  v.x = out_bits_rt(o[0] * inv, f16) | (out_bits_rt(o[1] * inv, f16) << 16);
+  v.y = out_bits_rt(o[2] * inv, f16) | (out_bits_rt(o[3] * inv, f16) << 16);
+  v.z = out_bits_rt(o[4] * inv, f16) | (out_bits_rt(o[5] * inv, f16) << 16);
+  v.w = out_bits_rt(o[6] * inv, f16) | (out_bits_rt(o[7] * inv, f16) << 16);
+  *out = v;
+}
+
 }  // namespace nvamd

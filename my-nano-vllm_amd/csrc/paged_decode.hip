@@ -1003,6 +1003,15 @@ __global__ __launch_bounds__(256) void decode_sk_merge_kernel(MqParams p) {
   sk_merge_one(p, b, gw - b * per_seq, threadIdx.x & 63);
 }
 
+// Decode with G <= 4: one wave per (sequence, kv head), its G heads at once.
+__global__ __launch_bounds__(256) void decode_sk_merge_heads_kernel(MqParams p) {
+  // 32-bit indices: the launch checks num_seqs * Hkv < 2^31
+  const int gw = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  if (gw >= p.num_seqs * p.Hkv) return;
+  const int b = gw / p.Hkv;
+  sk_merge_heads(p, b, gw - b * p.Hkv, threadIdx.x & 63);
+}
+
 namespace {
 template <int NCB, int HG, bool QL>
 int sk_occupancy() {
@@ -1078,7 +1087,11 @@ hipError_t launch_decode_sk(const MqParams& p, int ncb, bool merge, const Prefil
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (!merge) return hipSuccess;  // the caller's next launch merges
-  hipLaunchKernelGGL(decode_sk_merge_kernel, dim3((unsigned)merge_wgs), dim3(256), 0, stream, p);
+  if (!varlen && p.G <= 4)
+    hipLaunchKernelGGL(decode_sk_merge_heads_kernel, dim3((unsigned)(((int64_t)p.num_seqs * p.Hkv + 3) / 4)),
+                       dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL(decode_sk_merge_kernel, dim3((unsigned)merge_wgs), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 
