@@ -9,7 +9,8 @@ the block-table row and context length of every sequence.  One decode call
 is two launches: the balanced stream-K pass (``decode_sk_kernel<1,8,QL>``,
 one persistent workgroup per CU streaming an equal share of the KV stages)
 and the merge pass for sequences cut between workgroups
-(``decode_sk_merge_kernel``).  The HIP-event time of a call covers both, so
+(``decode_sk_merge_heads_kernel``: one wave per sequence and kv head).  The
+HIP-event time of a call covers both, so
 ``roofline.achieved`` is the algorithmic bytes over the two launches
 together (a lower bound on the stream-K kernel's own rate).
 
@@ -743,7 +744,7 @@ def main():
                     roofline=dict(bound="hbm", achieved=round(res["gbs"], 2), peak=HBM_PEAK_GBS,
                                   unit="GB/s", frac=round(res["gbs"] / HBM_PEAK_GBS, 4),
                                   traffic=_traffic_from_profile(),
-                                  kernel="decode_sk_kernel<1,8,QL> + decode_sk_merge_kernel (one decode call)",
+                                  kernel="decode_sk_kernel<1,8,QL> + decode_sk_merge_heads_kernel (one decode call)",
                                   algorithmic_bytes_per_launch=res["bytes"]),
                     config=dict(workload=wl.name, batch=wl.num_seqs, num_heads=wl.num_heads,
                                 num_kv_heads=wl.num_kv_heads, head_dim=128, block_size=wl.block_size,
@@ -764,7 +765,7 @@ def main():
                                           ms_per_step=round(res["ms"], 5), gbs=round(res["gbs"], 2),
                                           frac_hbm_peak=round(res["gbs"] / HBM_PEAK_GBS, 4),
                                           algorithmic_bytes_per_step=res["bytes"],
-                                          kernels="decode_sk_kernel<1,8,QL> + decode_sk_merge_kernel")
+                                          kernels="decode_sk_kernel<1,8,QL> + decode_sk_merge_heads_kernel")
         del pools
         torch.cuda.empty_cache()
 
