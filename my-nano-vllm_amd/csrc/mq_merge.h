@@ -196,12 +196,14 @@ __device__ __forceinline__ void sk_merge_one(const MqParams& p, int b, int idx, 
   const bool may_be_empty = T < W;
   const float* base = p.sk_part + (int64_t)(hh * p.sk_cols + col) * kSkSlotFloats;
   const int64_t wstride = (int64_t)HG * p.sk_cols * kSkSlotFloats;
-  // Contributors in chunks of 8: all of a chunk's loads (lane j < 8 reads
-  // (m, l) of contributor j, every lane its 2 dims of each) are issued
-  // before any is used, so a chunk costs one memory round trip.
+  // Contributors in chunks of 16 (one DPP row): all of a chunk's loads
+  // (lane j < 16 reads (m, l) of contributor j, every lane its 2 dims of
+  // each) are issued before any is used, so a chunk costs one memory round
+  // trip (speculative rows' pairs have up to ~14 contributors).
+  constexpr int kChunk = 16;
   float M = -INFINITY, Lsum = 0.f, o0 = 0.f, o1 = 0.f;
-  for (int w0 = wf; w0 <= wl; w0 += 8) {
-    const int cnt = min(8, wl - w0 + 1);
+  for (int w0 = wf; w0 <= wl; w0 += kChunk) {
+    const int cnt = min(kChunk, wl - w0 + 1);
     float mi = -INFINITY, li = 0.f;
     uint32_t skip = 0;  // bit j: contributor j has an empty range (only when T < W)
     if (may_be_empty) {
@@ -211,9 +213,9 @@ __device__ __forceinline__ void sk_merge_one(const MqParams& p, int b, int idx, 
             sk_range_start<uint32_t>(w0 + j + 1, (uint32_t)T, W, a))
           skip |= 1u << j;
     }
-    uint32_t a[8];  // dims 2 lane, 2 lane + 1 of contributor j's acc / l (fp16)
+    uint32_t a[kChunk];  // dims 2 lane, 2 lane + 1 of contributor j's acc / l (fp16)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < kChunk; ++j) {
       a[j] = 0u;
       if (j < cnt && !((skip >> j) & 1u)) {
         const int w = w0 + j;
@@ -225,7 +227,7 @@ __device__ __forceinline__ void sk_merge_one(const MqParams& p, int b, int idx, 
         }
       }
     }
-    // lanes 0..7 hold the chunk's values (the rest -inf and 0): DPP inside
+    // lanes 0..15 hold the chunk's values (the rest -inf and 0): DPP inside
     // the first row, then lane 0's result read by every lane
     const float Mp = readlane_f32(row16_max(mi), 0);
     const float Mn = fmaxf(M, Mp);
@@ -239,7 +241,7 @@ __device__ __forceinline__ void sk_merge_one(const MqParams& p, int b, int idx, 
     const float lw = li * wi;
     Lsum += readlane_f32(row16_sum(lw), 0);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {  // weight of a normalised partial: w_j * l_j
+    for (int j = 0; j < kChunk; ++j) {  // weight of a normalised partial: w_j * l_j
       const float wk = readlane_f32(lw, j);
       const f16x2 h = __builtin_bit_cast(f16x2, a[j]);
       o0 += wk * (float)h.x;

@@ -737,58 +737,66 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
     }
     __syncthreads();
     if (!s_last) return;
-    // (m, l) of every piece in one round trip, then the pieces' accumulators
-    // with the next piece's loads in flight while one is added
+    // (m, l) of every piece in one round trip, the first pieces' accumulators
+    // in flight behind them, then each piece added while later ones load.
+    // The merge is instantiated per piece count and unrolled, so that every
+    // load is unconditional, exactly the item's pieces are read, and each wait
+    // counts exactly the loads issued after the ones it needs.
     auto ml_off = [&](int j) { return (int)((uint32_t)j * piece_stride + 32u * 4u * kLanes + 8u * (uint32_t)tid); };
     auto acc_off = [&](int j, int w4) { return (int)((uint32_t)j * piece_stride + 16u * (uint32_t)(w4 * kLanes + tid)); };
-    float mj[kPrefillMaxPieces], lj[kPrefillMaxPieces];
+    auto load_piece = [&](u32x4 (&dst)[8], int j) {
 #pragma unroll
-    for (int j = 0; j < kPrefillMaxPieces; ++j) {
-      const f32x2 ml = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(pr, ml_off(min(j, n_pieces - 1)),
-                                                                                     0, kSc1));
-      mj[j] = (j < n_pieces) ? ml.x : -INFINITY;
-      lj[j] = (j < n_pieces) ? ml.y : 0.f;
-    }
-    float M = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < kPrefillMaxPieces; ++j) M = fmaxf(M, mj[j]);
-    const float Ms = (M == -INFINITY) ? 0.f : M;
+      for (int w4 = 0; w4 < 8; ++w4)
+        dst[w4] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, acc_off(j, w4), 0, kSc1));
+    };
     float L = 0.f;
+    auto merge_pieces = [&](auto n_const) {
+      constexpr int N = decltype(n_const)::value;
+      constexpr int R = N < 3 ? N : 3;  // pieces whose accumulators are in flight (32 VGPRs each)
+      f32x2 ml[N];
 #pragma unroll
-    for (int db = 0; db < 4; ++db) acc[db] = f32x16{};
-    u32x4 nxt[8];
+      for (int j = 0; j < N; ++j)
+        ml[j] = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(pr, ml_off(j), 0, kSc1));
+      u32x4 ring[R][8];
 #pragma unroll
-    for (int w4 = 0; w4 < 8; ++w4)
-      nxt[w4] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, acc_off(0, w4), 0, kSc1));
-    for (int j = 0; j < n_pieces; ++j) {
-      u32x4 cur[8];
+      for (int j = 0; j < R; ++j) load_piece(ring[j], j);
+      float M = -INFINITY;
 #pragma unroll
-      for (int w4 = 0; w4 < 8; ++w4) cur[w4] = nxt[w4];
-      if (j + 1 < n_pieces) {
+      for (int j = 0; j < N; ++j) M = fmaxf(M, ml[j].x);
+      const float Ms = (M == -INFINITY) ? 0.f : M;
 #pragma unroll
-        for (int w4 = 0; w4 < 8; ++w4)
-          nxt[w4] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, acc_off(j + 1, w4), 0, kSc1));
-      }
-      float mjj = mj[0], ljj = lj[0];
+      for (int db = 0; db < 4; ++db) acc[db] = f32x16{};
 #pragma unroll
-      for (int q = 1; q < kPrefillMaxPieces; ++q) {
-        mjj = (q == j) ? mj[q] : mjj;
-        ljj = (q == j) ? lj[q] : ljj;
-      }
-      const float wj = (mjj == -INFINITY) ? 0.f : ljj * fast_exp2(mjj - Ms);
-      L += wj;
+      for (int j = 0; j < N; ++j) {
+        u32x4 cur[8];
 #pragma unroll
-      for (int w4 = 0; w4 < 8; ++w4) {
-        const u32x4 hv = cur[w4];
-        const int db = w4 >> 1, i0 = 8 * (w4 & 1);
-        const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
+        for (int w4 = 0; w4 < 8; ++w4) cur[w4] = ring[j % R][w4];
+        if (j + R < N) load_piece(ring[j % R], j + R);
+        const float wj = (ml[j].x == -INFINITY) ? 0.f : ml[j].y * fast_exp2(ml[j].x - Ms);
+        L += wj;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const f16x2 h2 = __builtin_bit_cast(f16x2, hw[e]);
-          acc[db][i0 + 2 * e] += wj * (float)h2.x;
-          acc[db][i0 + 2 * e + 1] += wj * (float)h2.y;
+        for (int w4 = 0; w4 < 8; ++w4) {
+          const u32x4 hv = cur[w4];
+          const int db = w4 >> 1, i0 = 8 * (w4 & 1);
+          const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const f16x2 h2 = __builtin_bit_cast(f16x2, hw[e]);
+            acc[db][i0 + 2 * e] += wj * (float)h2.x;
+            acc[db][i0 + 2 * e + 1] += wj * (float)h2.y;
+          }
         }
       }
+    };
+    static_assert(kPrefillMaxPieces == 8, "one merge instance per piece count 2 .. 8");
+    switch (n_pieces) {  // 2 <= n_pieces <= kPrefillMaxPieces (the schedule's bound)
+      case 2: merge_pieces(std::integral_constant<int, 2>{}); break;
+      case 3: merge_pieces(std::integral_constant<int, 3>{}); break;
+      case 4: merge_pieces(std::integral_constant<int, 4>{}); break;
+      case 5: merge_pieces(std::integral_constant<int, 5>{}); break;
+      case 6: merge_pieces(std::integral_constant<int, 6>{}); break;
+      case 7: merge_pieces(std::integral_constant<int, 7>{}); break;
+      default: merge_pieces(std::integral_constant<int, 8>{}); break;
     }
     l_run = L;
   }
