@@ -96,11 +96,13 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restri
 // Block-scaled GEMM
 // ---------------------------------------------------------------------------
 // Tile shape: WN x WM waves, each TN x TM fragments of 16 x 16 (features x
-// tokens): BN = 16 TN WN features, BM = 16 TM WM tokens per workgroup.
-template <int WN, int WM, int TN, int TM>
+// tokens): BN = 16 TN WN features, BM = 16 TM WM tokens per workgroup; a ring
+// of S stages (S - 1 K blocks in flight while one is computed).
+template <int WN, int WM, int TN, int TM, int S = 2>
 struct GemmTile {
   static constexpr int kWaves = WN * WM;
   static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kStages = S;
   static constexpr int BN = 16 * TN * WN;
   static constexpr int BM = 16 * TM * WM;
   static constexpr int kWBytes = BN * kFp8Block;   // one K block of the weight tile
@@ -111,25 +113,31 @@ struct GemmTile {
   static constexpr int kWLoads = kWBytes / 1024 / kWaves;  // 1 KiB loads per wave per stage
   static constexpr int kXLoads = kXBytes / 1024 / kWaves;
   static constexpr int kLoads = kWLoads + kXLoads;
-  static constexpr int kWBlocks = (BN + kFp8Block - 1) / kFp8Block;  // weight-scale rows spanned
+  // A tile whose width neither divides nor is a multiple of the 128-row
+  // weight block (96) can straddle two blocks: its fragments then take their
+  // scales one by one.
+  static constexpr bool kStraddle = kFp8Block % BN != 0 && BN % kFp8Block != 0;
+  static constexpr int kWBlocks = (BN + kFp8Block - 1) / kFp8Block + (kStraddle ? 1 : 0);  // weight-scale rows spanned
   static_assert(kWBytes % (1024 * kWaves) == 0 && kXBytes % (1024 * kWaves) == 0, "whole loads per wave");
-  static_assert(BN <= kFp8Block || BN % kFp8Block == 0, "a fragment never straddles two weight blocks");
+  static_assert(BN <= kFp8Block || BN % kFp8Block == 0, "tiles wider than a block are whole blocks");
+  static_assert(kFp8Block % 16 == 0, "a fragment never straddles two weight blocks");
   static_assert(kWaves >= kSxLoads, "one scale load per wave");
+  static_assert(S >= 2, "a ring of at least two stages");
 };
 
-template <int WN, int WM, int TN, int TM>
-constexpr int64_t gemm_scale_offset() { return 2 * GemmTile<WN, WM, TN, TM>::kStage; }
+template <int WN, int WM, int TN, int TM, int S = 2>
+constexpr int64_t gemm_scale_offset() { return (int64_t)S * GemmTile<WN, WM, TN, TM, S>::kStage; }
 
 __host__ __device__ constexpr int64_t round_up_1k(int64_t b) { return (b + 1023) & ~(int64_t)1023; }
 
-// LDS bytes of a launch: two stages (weight tile, activation tile, and per
+// LDS bytes of a launch: S stages (weight tile, activation tile, and per
 // token row the dword of x_scale that holds its scale for the K block), then
 // the weight scales [kWBlocks, Kc] (bf16, from up to 7 elements earlier,
 // rounded up to whole 1 KiB loads).
-template <int WN, int WM, int TN, int TM>
+template <int WN, int WM, int TN, int TM, int S = 2>
 int64_t gemm_lds_bytes(int Kc) {
-  using T = GemmTile<WN, WM, TN, TM>;
-  return 2 * T::kStage + round_up_1k(((int64_t)T::kWBlocks * Kc + 8) * 2);
+  using T = GemmTile<WN, WM, TN, TM, S>;
+  return (int64_t)S * T::kStage + round_up_1k(((int64_t)T::kWBlocks * Kc + 8) * 2);
 }
 
 // Granule swizzle of a staged 128-byte row r: granule g sits at position
@@ -149,9 +157,9 @@ __device__ __forceinline__ i32x8 read_frag(const uint8_t* rows, int r, int q) {
   return i32x8{(int)a.x, (int)a.y, (int)a.z, (int)a.w, (int)b.x, (int)b.y, (int)b.z, (int)b.w};
 }
 
-template <int WN, int WM, int TN, int TM, bool F16_OUT>
+template <int WN, int WM, int TN, int TM, int S, bool F16_OUT>
 __global__ __launch_bounds__(64 * WN * WM) void block_gemm_kernel(Fp8GemmParams p) {
-  using T = GemmTile<WN, WM, TN, TM>;
+  using T = GemmTile<WN, WM, TN, TM, S>;
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   const uint32_t lds0 = wave_uniform((int)lds_addr(smem));
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_uniform(tid >> 6);
@@ -171,8 +179,10 @@ __global__ __launch_bounds__(64 * WN * WM) void block_gemm_kernel(Fp8GemmParams 
   // weight scales from a 16-byte aligned element (sw_shift elements before the tile's first)
   const int64_t sw_first = (int64_t)(n0 / kFp8Block) * Kc;
   const int sw_shift = (int)(sw_first & 7);
-  const u32x4 rsw =
-      rsrc_words(p.w_scale + (sw_first - sw_shift), (uint32_t)((((int64_t)T::kWBlocks * Kc + sw_shift) * 2 + 3) & ~3ll));
+  // kWBlocks rows, or to the array's end (a straddling tile's second row may
+  // not exist: the last tile need not straddle)
+  const int64_t sw_elems = min((int64_t)T::kWBlocks * Kc + sw_shift, (int64_t)(p.N / kFp8Block) * Kc - (sw_first - sw_shift));
+  const u32x4 rsw = rsrc_words(p.w_scale + (sw_first - sw_shift), (uint32_t)((sw_elems * 2 + 3) & ~3ll));
 
   // fetch offsets: load i of this wave covers tile rows 8 (wave + kWaves i) ..
   // + 7; lane l -> row + l / 8, LDS granule position l % 8, global granule
@@ -201,10 +211,12 @@ __global__ __launch_bounds__(64 * WN * WM) void block_gemm_kernel(Fp8GemmParams 
   };
 
   // weight scales [kWBlocks x Kc], loaded once
-  const uint32_t sw_lds = lds0 + (uint32_t)gemm_scale_offset<WN, WM, TN, TM>();
+  const uint32_t sw_lds = lds0 + (uint32_t)gemm_scale_offset<WN, WM, TN, TM, S>();
   for (int i = wave; i < (int)(round_up_1k(((int64_t)T::kWBlocks * Kc + 8) * 2) / 1024); i += T::kWaves)
     dma_load16_keep(rsw, 1024u * i + 16u * lane, sw_lds + 1024u * i);
-  issue_stage(0, 0);
+#pragma unroll
+  for (int st = 0; st < S - 1; ++st)
+    if (st < Kc) issue_stage(st, st);
 
   f32x4 acc[TN][TM];
 #pragma unroll
@@ -213,39 +225,56 @@ __global__ __launch_bounds__(64 * WN * WM) void block_gemm_kernel(Fp8GemmParams 
     for (int j = 0; j < TM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int q = lane >> 4, r16 = lane & 15;
-  const uint16_t* sw_rows = reinterpret_cast<const uint16_t*>(smem + gemm_scale_offset<WN, WM, TN, TM>());
-  const int wblk = T::BN <= kFp8Block ? 0 : (wn * TN * 16) / kFp8Block;  // the wave's weight block in the tile
+  const uint16_t* sw_rows = reinterpret_cast<const uint16_t*>(smem + gemm_scale_offset<WN, WM, TN, TM, S>());
+  // weight block (row of sw_rows) of the wave's fragments: one for the whole
+  // wave, or one per fragment when the tile can straddle two blocks
+  const int wblk = T::BN <= kFp8Block ? 0 : (wn * TN * 16) / kFp8Block;
+  int fblk[TN];
+#pragma unroll
+  for (int i = 0; i < TN; ++i) fblk[i] = (n0 % kFp8Block + (wn * TN + i) * 16) / kFp8Block;
+  // loads of one stage by this wave (waves below kSxLoads issue one more: the
+  // wait below is then stricter than needed for them)
+  constexpr int kStageLoads = T::kWLoads + T::kXLoads;
 
   for (int kc = 0; kc < Kc; ++kc) {
     // one barrier per K block: past it, every wave's loads of stage kc have
-    // landed and every wave is done reading buffer (kc + 1) & 1 (stage kc - 1),
-    // which then receives stage kc + 1 while stage kc is computed
-    wait_vmcnt<0>();  // this wave's loads of stage kc (and of the scales)
+    // landed and every wave is done reading buffer (kc - 1) % S (stage
+    // kc - 1), which then receives stage kc + S - 1 while stage kc is computed
+    // (this wave's loads of stage kc, and of the scales, are done when at most
+    // the later stages' loads are outstanding; near the end fewer are issued)
+    if (kc + S - 2 < Kc) wait_vmcnt<(S - 2) * kStageLoads>();
+    else wait_vmcnt<0>();
     lds_barrier();
-    if (kc + 1 < Kc) issue_stage(kc + 1, (kc + 1) & 1);
-    const uint8_t* st = smem + (kc & 1) * T::kStage;
+    if (kc + S - 1 < Kc) issue_stage(kc + S - 1, (kc + S - 1) % S);
+    const uint8_t* st = smem + (kc % S) * T::kStage;
     const uint8_t* wrows = st + (wn * TN * 16) * kFp8Block;
     const uint8_t* xrows = st + T::kWBytes + (wm * TM * 16) * kFp8Block;
     const uint32_t* sx_dw = reinterpret_cast<const uint32_t*>(st + T::kWBytes + T::kXBytes);
     const float sw = bf16_bits_to_f32(sw_rows[sw_shift + wblk * Kc + kc]);
-    float s[TM];
+    float sx[TM];
     i32x8 b[TM];
 #pragma unroll
     for (int j = 0; j < TM; ++j) {
       const int row = wm * TM * 16 + 16 * j + r16;
       const uint32_t d = sx_dw[row];
-      s[j] = bf16_bits_to_f32((row * Kc + kc) & 1 ? d >> 16 : d & 0xFFFFu) * sw;  // exact
+      sx[j] = bf16_bits_to_f32((row * Kc + kc) & 1 ? d >> 16 : d & 0xFFFFu);
       b[j] = read_frag(xrows + 16 * j * kFp8Block, r16, q);
     }
+    float s[TM];
+#pragma unroll
+    for (int j = 0; j < TM; ++j) s[j] = sx[j] * sw;  // exact (two bf16 values)
 #pragma unroll
     for (int i = 0; i < TN; ++i) {
       const i32x8 a = read_frag(wrows + 16 * i * kFp8Block, r16, q);
+      float swi = sw;
+      if constexpr (T::kStraddle) swi = bf16_bits_to_f32(sw_rows[sw_shift + fblk[i] * Kc + kc]);
 #pragma unroll
       for (int j = 0; j < TM; ++j) {
         const f32x4 part = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
             a, b[j], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
+        const float sij = T::kStraddle ? sx[j] * swi : s[j];  // exact
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[i][j][e] = __builtin_fmaf(part[e], s[j], acc[i][j][e]);
+        for (int e = 0; e < 4; ++e) acc[i][j][e] = __builtin_fmaf(part[e], sij, acc[i][j][e]);
       }
     }
   }
@@ -505,23 +534,32 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restr
 //   3: 2 x 1 waves, 2 x 1 fragments ->  64 x 16
 // (A 256 x 128 tile on 4 waves was slower than 1 at every size measured:
 // with one wave per SIMD neither the loads nor the FMAs overlap the MFMAs.)
-constexpr int kGemmConfigs = 4;
-constexpr int kGemmBN[kGemmConfigs] = {256, 128, 128, 64};
-constexpr int kGemmBM[kGemmConfigs] = {256, 64, 32, 16};
+// and, outside that order, for 64 < M <= 192 tokens:
+//   4: 2 x 6 waves, 3 x 2 fragments -> 96 x 192 (all the tokens), a ring of 4
+//      stages: a K block of 192 tokens is ~0.1 us of MFMA work per CU, so
+//      with one stage in flight every block waits a full load round trip;
+//      three stages in flight keep the weight stream going, and with N / 96
+//      tiles (a multiple of the CUs for Qwen3-8B gate/up) each weight byte is
+//      read once.
+constexpr int kGemmConfigs = 5;
+constexpr int kGemmOrdered = 4;  // configurations 0 .. 3 form the size order
+constexpr int kGemmBN[kGemmConfigs] = {256, 128, 128, 64, 96};
+constexpr int kGemmBM[kGemmConfigs] = {256, 64, 32, 16, 192};
 
 int64_t config_lds_bytes(int c, int Kc) {
   switch (c) {
     case 0: return gemm_lds_bytes<2, 4, 8, 4>(Kc);
     case 1: return gemm_lds_bytes<2, 2, 4, 2>(Kc);
     case 2: return gemm_lds_bytes<4, 1, 2, 2>(Kc);
-    default: return gemm_lds_bytes<2, 1, 2, 1>(Kc);
+    case 3: return gemm_lds_bytes<2, 1, 2, 1>(Kc);
+    default: return gemm_lds_bytes<2, 6, 3, 2, 4>(Kc);
   }
 }
 
-template <int WN, int WM, int TN, int TM, bool F16_OUT>
+template <int WN, int WM, int TN, int TM, int S, bool F16_OUT>
 hipError_t launch_config(const Fp8GemmParams& p, int64_t lds, hipStream_t stream) {
-  using T = GemmTile<WN, WM, TN, TM>;
-  auto kern = block_gemm_kernel<WN, WM, TN, TM, F16_OUT>;
+  using T = GemmTile<WN, WM, TN, TM, S>;
+  auto kern = block_gemm_kernel<WN, WM, TN, TM, S, F16_OUT>;
   static std::atomic<int64_t> lds_set{0};  // largest dynamic LDS size granted so far
   if (lds > lds_set.load(std::memory_order_relaxed)) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -675,10 +713,15 @@ hipError_t launch_fp8_act_quant(const void* x, int64_t x_stride, bool f16_in, vo
 }
 
 int fp8_gemm_pick_config(int64_t M, int64_t N, int Kc, int cus, int64_t lds_limit) {
+  // 64 < M <= 192 with whole 96-feature tiles covering the CUs: the deep-ring
+  // tile over all the tokens
+  if (M > 64 && M <= kGemmBM[4] && N % kGemmBN[4] == 0 && N / kGemmBN[4] >= cus &&
+      config_lds_bytes(4, Kc) <= lds_limit)
+    return 4;
   // the largest tile whose grid still covers the CUs and whose LDS fits;
   // otherwise the smallest tile that fits
   int best = -1;
-  for (int c = 0; c < kGemmConfigs; ++c) {
+  for (int c = 0; c < kGemmOrdered; ++c) {
     if (N % kGemmBN[c] != 0 || config_lds_bytes(c, Kc) > lds_limit) continue;
     best = c;
     if ((N / kGemmBN[c]) * ((M + kGemmBM[c] - 1) / kGemmBM[c]) >= cus) return c;
@@ -694,14 +737,16 @@ hipError_t launch_fp8_block_gemm(const Fp8GemmParams& p, int config, bool f16_ou
     return hipErrorInvalidValue;
   const int64_t lds = config_lds_bytes(config, p.Kc);
   switch (config * 2 + (f16_out ? 1 : 0)) {
-    case 0: return launch_config<2, 4, 8, 4, false>(p, lds, stream);
-    case 1: return launch_config<2, 4, 8, 4, true>(p, lds, stream);
-    case 2: return launch_config<2, 2, 4, 2, false>(p, lds, stream);
-    case 3: return launch_config<2, 2, 4, 2, true>(p, lds, stream);
-    case 4: return launch_config<4, 1, 2, 2, false>(p, lds, stream);
-    case 5: return launch_config<4, 1, 2, 2, true>(p, lds, stream);
-    case 6: return launch_config<2, 1, 2, 1, false>(p, lds, stream);
-    default: return launch_config<2, 1, 2, 1, true>(p, lds, stream);
+    case 0: return launch_config<2, 4, 8, 4, 2, false>(p, lds, stream);
+    case 1: return launch_config<2, 4, 8, 4, 2, true>(p, lds, stream);
+    case 2: return launch_config<2, 2, 4, 2, 2, false>(p, lds, stream);
+    case 3: return launch_config<2, 2, 4, 2, 2, true>(p, lds, stream);
+    case 4: return launch_config<4, 1, 2, 2, 2, false>(p, lds, stream);
+    case 5: return launch_config<4, 1, 2, 2, 2, true>(p, lds, stream);
+    case 6: return launch_config<2, 1, 2, 1, 2, false>(p, lds, stream);
+    case 7: return launch_config<2, 1, 2, 1, 2, true>(p, lds, stream);
+    case 8: return launch_config<2, 6, 3, 2, 4, false>(p, lds, stream);
+    default: return launch_config<2, 6, 3, 2, 4, true>(p, lds, stream);
   }
 }
 

@@ -16,11 +16,14 @@ missing K block errs by about 2^-3.5 of it.
 
 Shapes are chosen so that on a 256-CU MI355X the library picks each of its
 tile shapes (256x256, 128x64, 128x32, 64x16 features x tokens): it takes the
-largest tile whose grid still covers the CUs.  Products with at most 256
-tokens take the small-M kernel instead (weights streamed once; K split over
-workgroups with fp32 partials added in split order when the workspace allows):
-its cases cover 1 to 256 tokens, 2, 4 and 8 compute waves, splits and no
-workspace.
+largest tile whose grid still covers the CUs.  65 to 192 tokens with at least
+a CU's worth of 96-feature tiles take the 96x192 tile with a 4-stage ring
+(tiles straddle the 128-row weight blocks, so fragments take their own
+scales; K shorter than the ring).  Products with at most 256 tokens whose tile
+grid would leave CUs idle take the small-M kernel instead (weights streamed
+once; K split over workgroups with fp32 partials added in split order when the
+workspace allows): its cases cover 1 to 256 tokens, 2, 4 and 8 compute waves,
+splits and no workspace.
 """
 import numpy as np
 import pytest
@@ -147,13 +150,16 @@ def test_act_quant_unit_scale_all_patterns_and_strided_rows():
 # 128x64: (1024, 2048, 256); 128x32: (1024, 1024, 128); 64x16: (300, 128, 256)
 TILE_SHAPES = [(4096, 4096, 256), (4096, 4096, 640), (1024, 2048, 256), (1024, 1024, 128), (300, 128, 256)]
 # at most 256 tokens: the Qwen3-8B qkv and down products at 192 tokens take the small-M kernel (down with K
-# split over workgroups), gate/up the 128x64 tile (its grid covers the CUs); 256 tokens (16 token fragments),
-# one token (K split), ragged token counts and odd K block counts on the small-M kernel
+# split over workgroups), gate/up the 96x192 ring tile; 256 tokens (16 token fragments), one token (K split),
+# ragged token counts and odd K block counts on the small-M kernel
 SKINNY_SHAPES = [(192, 6144, 4096), (192, 24576, 4096), (192, 4096, 12288), (256, 1024, 4096), (1, 4096, 4096),
                  (24, 256, 512), (1, 128, 128), (77, 2048, 1664), (130, 512, 3200)]
+# the 96x192 ring tile: ragged tokens with an odd number of K blocks, K shorter than the ring (2 and 1 blocks),
+# 65 tokens (its lower bound)
+RING_SHAPES = [(100, 24576, 640), (150, 24576, 256), (192, 24576, 128), (65, 24576, 1024)]
 
 
-@pytest.mark.parametrize("M,N,K", TILE_SHAPES + SKINNY_SHAPES)
+@pytest.mark.parametrize("M,N,K", TILE_SHAPES + SKINNY_SHAPES + RING_SHAPES)
 def test_gemm_exact_integer_case(M, N, K):
     """Small-integer codes, power-of-two scales: every fp32 step is exact, so
     the GPU must equal the oracle bit for bit (a transposed operand, a wrong
@@ -172,7 +178,8 @@ def test_gemm_exact_integer_case(M, N, K):
 
 @pytest.mark.parametrize("M,N,K,out_dtype", [(4000, 4096, 384, torch.bfloat16), (1000, 2048, 512, torch.bfloat16),
                                              (77, 1024, 1024, torch.float16), (5, 384, 4096, torch.bfloat16),
-                                             (130, 256, 12288, torch.bfloat16)])
+                                             (130, 256, 12288, torch.bfloat16), (160, 24576, 768, torch.bfloat16),
+                                             (96, 24576, 512, torch.float16)])
 def test_gemm_matches_oracle(M, N, K, out_dtype):
     """Random codes (all finite E4M3FN values) and scales over five decades
     (two for the fp16 output, which must stay below 65504); ragged M, K up to
