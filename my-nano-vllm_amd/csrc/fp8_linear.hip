@@ -201,8 +201,13 @@ __global__ __launch_bounds__(64 * WN * WM) void block_gemm_kernel(Fp8GemmParams 
   auto issue_stage = [&](int kc, int buf) {
     const uint32_t base = lds0 + (uint32_t)(buf * T::kStage);
 #pragma unroll
-    for (int i = 0; i < T::kWLoads; ++i)
-      dma_load16_keep(rw, w_off(i, kc), base + (uint32_t)(1024 * (wave + T::kWaves * i)));
+    for (int i = 0; i < T::kWLoads; ++i) {
+      // a ring tile (S > 2) covers all the tokens, so its weight bytes are
+      // read once: non-temporal, leaving the L2 to the activation rows every
+      // workgroup of the XCD reads
+      if constexpr (S > 2) dma_load16(rw, w_off(i, kc), base + (uint32_t)(1024 * (wave + T::kWaves * i)));
+      else dma_load16_keep(rw, w_off(i, kc), base + (uint32_t)(1024 * (wave + T::kWaves * i)));
+    }
 #pragma unroll
     for (int i = 0; i < T::kXLoads; ++i)
       dma_load16_keep(rx, x_off(i, kc), base + (uint32_t)(T::kWBytes + 1024 * (wave + T::kWaves * i)));
