@@ -649,6 +649,20 @@ struct SkStage {
   static constexpr int kRing = kDepth * kSlot;
 };
 
+// Granule swizzle of stage row r (0..15): granule g of the row sits at
+// position g ^ sk_swz(r).  Rows are 512 or 1024 bytes, so every row starts on
+// the same LDS banks and the swizzle alone spreads the reads.  A K read takes
+// granules {c, c + 1} (or {c + 2, c + 3}) of rows 0..15 in 32 lanes:
+// sk_swz(r) >> 1 == r, so the 32 positions are distinct mod 32 granules
+// (512 bytes), and sk_swz(r) & 15 is a permutation of 0..15, so each 16-lane
+// half is distinct mod 16 too.  A V read takes rows e, e+4, e+8, e+12 (8
+// bytes of one granule column each): their swizzles differ in bits 3..4, so
+// the four rows sit on four different 128-byte lines of a 512-byte window.
+// Bits 0..2 permute within a 128-byte line and bits 3..4 move whole lines, so
+// each 8-lane group of a fetch still reads one whole 128-byte line.
+// (r & 7) put 32 lanes of a K read on 8 positions: a 4-way bank conflict.
+__device__ __forceinline__ int sk_swz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1) | ((r & 8) << 1); }
+
 // A prefill call with long sequences launches one workgroup more (index
 // sk_wgs, resident beside the sk_wgs stream-K workgroups) that writes the
 // prefill kernel's work list (items != nullptr).
@@ -744,7 +758,7 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p, PrefillP
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int row = (2 * wave + i) * S::kRowsPerLoad + lane / S::kLanesPerRow;
-    const int gran = (lane % S::kLanesPerRow) ^ (row & 7);
+    const int gran = (lane % S::kLanesPerRow) ^ sk_swz(row);
     fetch_off[i] = (uint32_t)row * (uint32_t)rs + 16u * (uint32_t)gran;
   }
 
@@ -831,11 +845,11 @@ __global__ __launch_bounds__(64 * HG) void decode_sk_kernel(MqParams p, PrefillP
   uint32_t k_rd[2], v_rd[4];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
-    k_rd[i] = (uint32_t)(r * S::kRowBytes + 16 * ((8 * wave + 4 * i + gam) ^ (r & 7)));
+    k_rd[i] = (uint32_t)(r * S::kRowBytes + 16 * ((8 * wave + 4 * i + gam) ^ sk_swz(r)));
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int rv = 4 * gam + e;
-    v_rd[e] = (uint32_t)(S::kHalf + rv * S::kRowBytes + 16 * ((8 * wave + (r >> 1)) ^ (rv & 7)) + 8 * (r & 1));
+    v_rd[e] = (uint32_t)(S::kHalf + rv * S::kRowBytes + 16 * ((8 * wave + (r >> 1)) ^ sk_swz(rv)) + 8 * (r & 1));
   }
 
   // ---- compute cursor: pair (cb_s, chg), stage co of cn, length cL -------------
