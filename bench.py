@@ -778,7 +778,7 @@ def main():
                                 tflops=round(res["tflops"], 2),
                                 frac_bf16_peak=round(res["tflops"] / BF16_PEAK_TFLOPS, 4),
                                 algorithmic_flops_per_step=res["flops"],
-                                kernels="decode_sk_kernel<2,8> (short-query rows, none here; one workgroup "
+                                kernels="decode_sk_kernel<2,4> (short-query rows, none here; one workgroup "
                                         "writes the work list) + varlen_prefill_kernel<true>")
         if not args.no_cpu_baseline:
             log("cpu baseline (oracle) on a sample of the prefill workload")
@@ -802,7 +802,7 @@ def main():
         extra["store"] = dict(workload=wl.name + " new tokens (8192 x 8 kv heads, strided K/V views of qkv)",
                               ms_per_step=round(res["ms"], 5), gbs=round(res["gbs"], 2),
                               frac_hbm_peak=round(res["gbs"] / HBM_PEAK_GBS, 4), algorithmic_bytes_per_step=res["bytes"],
-                              kernels="kv_store_fp8_kernel",
+                              kernels="kv_store_fp8_pair_kernel",
                               ceilings=dict(
                                   conversion_copy_ms=round(res["conversion_copy_ms"], 5),
                                   conversion_copy="torch bf16 -> float8_e4m3fn copy_ of the same 2 x 8192 x 8 x 128 "
@@ -843,7 +843,7 @@ def main():
             spec_rows_only=dict(ms_per_step=round(res_s["ms"], 5), algorithmic_bytes_per_step=spec_bytes,
                                 gbs=round(spec_bytes / (res_s["ms"] * 1e-3) / 1e9, 2),
                                 frac_hbm_peak=round(spec_bytes / (res_s["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)),
-            kernels="decode_sk_kernel<2,8> (speculative rows, stream-K; one workgroup writes the work list) + "
+            kernels="decode_sk_kernel<2,4> (speculative rows, stream-K; one workgroup writes the work list) + "
                     "varlen_prefill_kernel<true> (chunks, and the merge); speculative rows alone: decode_sk_kernel "
                     "+ decode_sk_merge_kernel")
         extra["contiguous_prefill"] = dict(
@@ -924,7 +924,7 @@ def main():
         extra["lm_head"] = dict(
             workload="the mixed step's LM-head rows (192 decode + 32 x 5 speculative + 3 prefill = 355), "
                      "Qwen3 vocabulary 151936, bf16 logits",
-            kernels="sample_kernel, select_rows_kernel",
+            kernels="sample_group_kernel + sample_group_pick_kernel, select_rows_kernel",
             sampler=dict(ms_per_step=round(res["ms"], 5), gbs=round(res["gbs"], 1),
                          frac_hbm_peak=round(res["gbs"] / HBM_PEAK_GBS, 4), algorithmic_bytes=res["bytes"],
                          reference_arithmetic_torch_ms=round(res["ms_torch"], 5)),
