@@ -52,6 +52,37 @@ hipStream_t stream_of(const at::Tensor& t) {
   return c10::hip::getCurrentHIPStream(t.device().index()).stream();
 }
 
+// The kernels take at most 32 query heads per kv head (G; the decode kernels
+// hold G query columns of a kv head in two 16-column MFMA blocks).  The
+// reference's kernels take any G, so a call with more runs as G / gs calls,
+// gs the largest divisor of G up to 32: call s takes query heads
+// j G + s gs .. j G + s gs + gs - 1 of every kv head j, as a contiguous copy
+// in which kv head j owns query heads j gs .. j gs + gs - 1, and its output
+// is copied back into those heads.  Each call streams the K/V again.  Returns
+// gs, or 0 when no split is needed (or the shapes are invalid: the checks of
+// the unsplit call report them).
+constexpr int64_t kMaxHeadsPerKvHead = 32;
+int64_t head_slice(int64_t num_heads, int64_t num_kv_heads) {
+  if (num_kv_heads <= 0 || num_heads % num_kv_heads != 0) return 0;
+  const int64_t g = num_heads / num_kv_heads;
+  if (g <= kMaxHeadsPerKvHead) return 0;
+  int64_t gs = kMaxHeadsPerKvHead;
+  while (g % gs != 0) --gs;
+  return gs;
+}
+
+// out[:, heads of slice s] = call(q[:, heads of slice s]) for every slice (see head_slice).
+template <typename F>
+void run_head_slices(const at::Tensor& q, at::Tensor& out, int64_t num_kv_heads, int64_t gs, F&& call) {
+  const int64_t rows = q.size(0), g = q.size(1) / num_kv_heads, d = q.size(2);
+  const at::Tensor qv = q.view({rows, num_kv_heads, g / gs, gs, d});
+  at::Tensor ov = out.view({rows, num_kv_heads, g / gs, gs, d});
+  for (int64_t s = 0; s < g / gs; ++s) {
+    const at::Tensor qs = qv.select(2, s).reshape({rows, num_kv_heads * gs, d});
+    ov.select(2, s).copy_(call(qs).view({rows, num_kv_heads, gs, d}));
+  }
+}
+
 void check_status(int32_t st, const char* what) {
   TORCH_CHECK(st == NVAMD_OK, what, " failed (status ", st, "): ", nvamd_last_error());
 }
@@ -113,6 +144,11 @@ at::Tensor decode(const at::Tensor& q_in, const at::Tensor& k_in, const at::Tens
   const at::Tensor q = q_in.contiguous(), k = k_in.contiguous(), v = v_in.contiguous();
   at::Tensor out = at::empty(q.sizes(), q.options());
   if (batch == 0) return out;
+  if (const int64_t gs = head_slice(num_heads, num_kv_heads)) {
+    run_head_slices(q, out, num_kv_heads, gs,
+                    [&](const at::Tensor& qs) { return decode(qs, k, v, bt, ctx, softmax_scale); });
+    return out;
+  }
   const at::OptionalDeviceGuard guard(q.device());
   const int64_t ws_n = nvamd_decode_workspace_bytes((int32_t)batch, (int32_t)num_heads, (int32_t)num_kv_heads,
                                                     (int32_t)max_num_blocks, (int32_t)block_size, 0);
@@ -164,6 +200,12 @@ at::Tensor prefill(const at::Tensor& q_in, const at::Tensor& k_in, const at::Ten
   const at::Tensor q = q_in.contiguous(), k = k_in.contiguous(), v = v_in.contiguous();
   at::Tensor out = at::empty(q.sizes(), q.options());
   if (num_tokens == 0 || num_seqs <= 0) return out;
+  if (const int64_t gs = head_slice(num_heads, num_kv_heads)) {
+    run_head_slices(q, out, num_kv_heads, gs, [&](const at::Tensor& qs) {
+      return prefill(qs, k, v, block_tables_in, cu_q, cu_k, max_seqlen_q, max_seqlen_k, softmax_scale);
+    });
+    return out;
+  }
   const at::OptionalDeviceGuard guard(q.device());
   const int64_t ws_n = nvamd_prefill_workspace_bytes(num_tokens, (int32_t)num_seqs, (int32_t)num_heads,
                                                      (int32_t)num_kv_heads, kv_cap, (int32_t)max_seqlen_q,
